@@ -1,0 +1,85 @@
+/* nwc_ops.h -- the C ABI of libnwc_ops.so for AMD Instinct MI355X (gfx950).
+ *
+ * A drop-in for the reference library parda21/NWC csrc/nwc_ops.cu (exports listed at nwc_ops.cu:27-39 and
+ * docs/format.md:176-188): the same symbol names, argument order, argument meaning and return codes, so the
+ * reference's ctypes bindings (nwc/nwc_torch.py:58-77) load this library unchanged.  Every pointer is a plain
+ * address; `stream` is a hipStream_t passed as void* (torch.cuda.current_stream().cuda_stream), work is ordered on
+ * it and no entry point synchronises the host.  The library allocates no device memory: outputs and the scratch
+ * buffer belong to the caller.  `elem` = element type (0 BF16, 1 fp8 e4m3fn) | layout << 4 (layouts 0, 1, 2).
+ * `block` must be 4096 (nwc_info(4)); K is the number of columns, n = M * K.
+ *
+ * Device entry points return 0, -1 for a shape the format cannot describe, or a hipError_t code of the launch.
+ */
+#ifndef NWC_OPS_H
+#define NWC_OPS_H
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Capability query.  0: format version (11), 1: states per lane (1), 2: table words (4096), 3: header bytes per
+ * block (32), 4: block size (4096), 5: elem parameter present (1), 6: layout 1 supported (1), 7: layout 2
+ * supported (1), other: -1.  Replaces nwc_ops.cu:100-106. */
+int nwc_info(int what);
+
+/* out[0..3] = [blocks, bytes of the raw plane `low` (without slack), scratch floats (Mp * CB), K16];
+ * -1 if M == 0, K == 0 or M > 2^32 - 1.  Replaces nwc_ops.cu:121-126. */
+int nwc_layout(uint64_t M, uint32_t K, int elem, uint64_t *out);
+
+/* Host encoder.  w: BF16 bits (uint16 [n]) or fp8 e4m3fn bytes (uint8 [n]), row-major M x K.  Writes
+ * psym[0..1023] (exp_of_rank / layout-2 rank tables), bases[nb], hdr[32 nb], data[.. return value), low[raw bytes];
+ * freq[0..1023] is cleared.  Returns the data length including 64 bytes of read-ahead slack, -1 for a bad shape,
+ * insufficient capacity or a lane stream longer than 255 words, -2 for NaN in fp8 input, -3 for a layout-2 lane with
+ * more than 255 exceptions.  Output bytes equal the reference encoder's.  Replaces nwc_ops.cu:245-320 (and
+ * encode2, :175-243). */
+int64_t nwc_encode(const void *w, uint64_t n, uint32_t K, int elem, uint16_t *freq, uint16_t *psym, uint32_t *bases,
+                   uint8_t *hdr, uint8_t *data, uint64_t data_cap, uint8_t *low);
+
+/* Host: the 4096-word decode table from psym (layout 2: the 4-word rank tables).  Replaces nwc_ops.cu:324-348. */
+void nwc_build_tab(const uint16_t *freq, const uint16_t *psym, int elem, uint32_t *lut);
+
+/* fp32 test path y[M] = W x; x fp32 [K16] (zero beyond K; layouts 1/2: [K32]).  Unlike the reference (memset +
+ * atomics, nwc_ops.cu:1110-1118) every y[m] is written exactly once, so no clearing is needed and the result is
+ * deterministic.  Replaces nwc_ops.cu:1110. */
+int nwc_matvec(void *stream, const uint8_t *data, const uint32_t *bases, const uint8_t *hdr, const uint32_t *tab,
+               const uint8_t *low, const float *x, float *y, uint64_t n, uint32_t block, uint32_t K, int elem);
+
+/* Decompression to BF16 [M x K16], row stride K16 (fp8: the unscaled fp8 values, exact in BF16).
+ * Replaces nwc_ops.cu:1121. */
+int nwc_dequant(void *stream, const uint8_t *data, const uint32_t *bases, const uint8_t *hdr, const uint32_t *tab,
+                const uint8_t *low, uint16_t *out, uint64_t n, uint32_t block, uint32_t K, int elem);
+
+/* Token path y = RNE_bf16(scale * (W x) + bias).  x: layout 0 fp32 [K16], layouts 1/2 BF16 [K32] (zero beyond K),
+ * passed through a float pointer as in the reference; bias BF16 [M] or NULL; scale fp32 [M] or NULL (fp8);
+ * scratch fp32 [Mp * CB] is accepted for ABI compatibility and not touched (the column-block partial sums are
+ * reduced inside the kernel); y BF16 [M].  Replaces nwc_ops.cu:1130. */
+int nwc_linear_bf16(void *stream, const uint8_t *data, const uint32_t *bases, const uint8_t *hdr, const uint32_t *tab,
+                    const uint8_t *low, const float *x, const uint16_t *bias, const float *scale, float *scratch,
+                    uint16_t *y, uint64_t n, uint32_t block, uint32_t K, int elem);
+
+/* Token path with x as BF16 for every layout (layout 0: BF16 [K16]; layouts 1/2: BF16 [K32]), otherwise as
+ * nwc_linear_bf16.  No counterpart in the reference, whose Python side converts x to fp32 for layout 0 with an
+ * extra kernel (nwc_torch.py:238-239); callers that hold BF16 activations use this one. */
+int nwc_linear_xbf16(void *stream, const uint8_t *data, const uint32_t *bases, const uint8_t *hdr, const uint32_t *tab,
+                     const uint8_t *low, const uint16_t *x, const uint16_t *bias, const float *scale, uint16_t *y,
+                     uint64_t n, uint32_t K, int elem);
+
+/* Rows ids[0..n_ids) -> BF16 [n_ids x K16] (embedding lookup from the compressed matrix); ids outside [0, M) leave
+ * their output row untouched, as in the reference.  0 for n_ids == 0.  Replaces nwc_ops.cu:1143. */
+int nwc_gather(void *stream, const uint8_t *data, const uint32_t *bases, const uint8_t *hdr, const uint32_t *tab,
+               const uint8_t *low, const int64_t *ids, uint32_t n_ids, uint16_t *out, uint64_t n, uint32_t block,
+               uint32_t K, int elem);
+
+/* Uncompressed fp8 weight-only matvec (the bandwidth baseline): y = RNE_bf16(scale * (W8 x)), w fp8 e4m3fn [M x K]
+ * row-major, scale fp32 [M], x fp32 [K16], y BF16 [M].  Replaces nwc_ops.cu:1163. */
+int nwc_ref_fp8(void *stream, const uint8_t *w, const float *scale, const float *x, uint16_t *y, uint64_t M, uint32_t K);
+
+/* Device set-up; returns the compute-unit count of the current device (0 without a usable GPU).  Called lazily by
+ * the launchers.  Replaces nwc_ops.cu:1170. */
+int nwc_setup(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

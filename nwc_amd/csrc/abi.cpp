@@ -1,0 +1,111 @@
+// abi.cpp -- device entry points of the C ABI (declared in include/nwc_ops.h): argument checks, launch plans and
+// dispatch to the kernel files.  Argument meaning and return codes follow parda21/NWC csrc/nwc_ops.cu:1045-1192.
+#include "nwc_launch.h"
+#include "nwc_ops.h"
+
+#include <atomic>
+
+using namespace nwc;
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::atomic<int> g_cus[kMaxDevices];
+
+int current_cus() {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 0;
+    int c = g_cus[dev].load(std::memory_order_relaxed);
+    if (c > 0) return c;
+    if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c <= 0) return 0;
+    g_cus[dev].store(c, std::memory_order_relaxed);
+    return c;
+}
+
+// nwc_ops.cu:1050: the fixed block of 4096 weights, M = n / K within 32 bits, and a known element type / layout
+bool shape_ok(uint64_t n, uint32_t block, uint32_t K, int elem) {
+    return block == kBlock && K != 0 && n % K == 0 && n / K >= 1 && n / K <= 0xFFFFFFFFull && elem_type(elem) <= 1 &&
+           elem_layout(elem) <= 2 && (elem & ~0xFF) == 0;
+}
+
+// Workgroup tile = G whole row groups.  Prefer at least two workgroups per CU (small matrices spread over the
+// whole chip), at most 32 blocks (16 waves) per workgroup, and an even block count so both halves of every wave
+// have a block.
+LaunchPlan plan_blocks(const Shape &f, int layout, int mode, int ncu) {
+    LaunchPlan p{};
+    p.layout = layout;
+    const uint32_t CB = f.CB, groups = f.groups();
+    uint32_t G = CB >= 32 ? 1u : 32u / CB;
+    while (G > 1 && (groups + G - 1) / G < 2u * (uint32_t)ncu) G--;
+    if (G > 1 && ((G * CB) & 1u)) G--;
+    if (G > groups) G = groups;
+    if (G == 0) G = 1;
+    const uint32_t blocks = G * CB;
+    p.G = G;
+    p.threads = 64u * std::min(16u, (blocks + 1) / 2);
+    p.grid = (groups + G - 1) / G;
+    p.lds = mode == kDequant ? 0u : G * f.rows * CB * 4u;
+    return p;
+}
+
+int run_blocks(int mode, bool xbf16, hipStream_t st, const uint8_t *data, const uint32_t *bases, const uint8_t *hdr,
+               const uint32_t *tab, const uint8_t *low, const void *x, const uint16_t *bias, const float *scale, void *out,
+               uint64_t n, uint32_t K, int elem) {
+    const int ncu = current_cus();
+    if (ncu <= 0) return (int)hipErrorNoDevice;
+    const int layout = elem_layout(elem), t = elem_type(elem);
+    const Shape f((uint32_t)(n / K), K, layout);
+    const LaunchPlan p = plan_blocks(f, layout, mode, ncu);
+    if (p.lds > 48u * 1024u) return -1;        // K beyond what one workgroup's partial sums fit (K > ~98k columns)
+    BlockArgs a{data, bases, hdr, tab, low, x, bias, scale, out, f.M, f.K, p.G};
+    return layout == 2 ? launch_fixed(p, t, mode, xbf16, a, st) : launch_prefix(p, t, mode, xbf16, a, st);
+}
+
+}  // namespace
+
+extern "C" int nwc_setup(void) { return current_cus(); }
+
+extern "C" int nwc_matvec(void *stream, const uint8_t *data, const uint32_t *bases, const uint8_t *hdr, const uint32_t *tab,
+                          const uint8_t *low, const float *x, float *y, uint64_t n, uint32_t block, uint32_t K, int elem) {
+    if (!shape_ok(n, block, K, elem)) return -1;
+    return run_blocks(kF32, false, (hipStream_t)stream, data, bases, hdr, tab, low, x, nullptr, nullptr, y, n, K, elem);
+}
+
+extern "C" int nwc_dequant(void *stream, const uint8_t *data, const uint32_t *bases, const uint8_t *hdr, const uint32_t *tab,
+                           const uint8_t *low, uint16_t *out, uint64_t n, uint32_t block, uint32_t K, int elem) {
+    if (!shape_ok(n, block, K, elem)) return -1;
+    return run_blocks(kDequant, true, (hipStream_t)stream, data, bases, hdr, tab, low, nullptr, nullptr, nullptr, out, n, K, elem);
+}
+
+extern "C" int nwc_linear_bf16(void *stream, const uint8_t *data, const uint32_t *bases, const uint8_t *hdr, const uint32_t *tab,
+                               const uint8_t *low, const float *x, const uint16_t *bias, const float *scale, float *scratch,
+                               uint16_t *y, uint64_t n, uint32_t block, uint32_t K, int elem) {
+    (void)scratch;
+    if (!shape_ok(n, block, K, elem)) return -1;
+    const bool xbf16 = elem_layout(elem) != 0;                    // layout 0 takes fp32 x, layouts 1/2 BF16 x
+    return run_blocks(kToken, xbf16, (hipStream_t)stream, data, bases, hdr, tab, low, x, bias, scale, y, n, K, elem);
+}
+
+extern "C" int nwc_linear_xbf16(void *stream, const uint8_t *data, const uint32_t *bases, const uint8_t *hdr, const uint32_t *tab,
+                                const uint8_t *low, const uint16_t *x, const uint16_t *bias, const float *scale, uint16_t *y,
+                                uint64_t n, uint32_t K, int elem) {
+    if (!shape_ok(n, kBlock, K, elem)) return -1;
+    return run_blocks(kToken, true, (hipStream_t)stream, data, bases, hdr, tab, low, x, bias, scale, y, n, K, elem);
+}
+
+extern "C" int nwc_gather(void *stream, const uint8_t *data, const uint32_t *bases, const uint8_t *hdr, const uint32_t *tab,
+                          const uint8_t *low, const int64_t *ids, uint32_t n_ids, uint16_t *out, uint64_t n, uint32_t block,
+                          uint32_t K, int elem) {
+    if (!shape_ok(n, block, K, elem)) return -1;
+    if (n_ids == 0) return 0;
+    if (current_cus() <= 0) return (int)hipErrorNoDevice;
+    GatherArgs a{data, bases, hdr, tab, low, ids, n_ids, out, (uint32_t)(n / K), K};
+    const int layout = elem_layout(elem), t = elem_type(elem);
+    return layout == 2 ? launch_gather_fixed(t, a, (hipStream_t)stream) : launch_gather_prefix(layout, t, a, (hipStream_t)stream);
+}
+
+extern "C" int nwc_ref_fp8(void *stream, const uint8_t *w, const float *scale, const float *x, uint16_t *y, uint64_t M, uint32_t K) {
+    if (M == 0 || K == 0 || M > 0xFFFFFFFFull) return -1;
+    if (current_cus() <= 0) return (int)hipErrorNoDevice;
+    return launch_ref_fp8(w, scale, x, y, (uint32_t)M, K, (hipStream_t)stream);
+}

@@ -1,0 +1,254 @@
+// nwc_device.h -- gfx950 building blocks shared by the kernels: the prefix-code window decoder, the staged decode
+// table, half-wave scans/reductions and BF16 helpers.
+//
+// Execution model: a wave64 carries two independent blocks, one per 32-lane half, because the format fixes 32 lane
+// streams per block (docs/format.md section 3).  All cross-lane traffic stays inside a half.
+#pragma once
+#include "nwc_format.h"
+
+namespace nwc {
+
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
+
+__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a), __builtin_bit_cast(bf16x2_t, b), c, false);
+}
+__device__ __forceinline__ float bf16_lo(uint32_t v) { return __uint_as_float(v << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t v) { return __uint_as_float(v & 0xFFFF0000u); }
+// round to nearest even (NaN stays NaN)
+__device__ __forceinline__ uint32_t f32_to_bf16_rne(float v) {
+    uint32_t u = __float_as_uint(v);
+    if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (u >> 16) | 0x40u;
+    u += 0x7FFFu + ((u >> 16) & 1u);
+    return u >> 16;
+}
+__device__ __forceinline__ uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel) { return __builtin_amdgcn_perm(hi, lo, sel); }
+
+// streaming (non-temporal) loads of plane data that is read exactly once
+typedef __attribute__((ext_vector_type(4))) uint32_t u32x4_t;
+typedef __attribute__((ext_vector_type(2))) uint32_t u32x2_t;
+__device__ __forceinline__ uint4 ldnt4(const void *p) {
+    const u32x4_t v = __builtin_nontemporal_load((const u32x4_t *)p);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint2 ldnt2(const void *p) {
+    const u32x2_t v = __builtin_nontemporal_load((const u32x2_t *)p);
+    return make_uint2(v.x, v.y);
+}
+__device__ __forceinline__ uint32_t ldnt1(const void *p) { return __builtin_nontemporal_load((const uint32_t *)p); }
+
+// Byte selectors for v_perm_b32(e, raw, sel): bytes 0-3 of `raw`, 4-7 of `e` (e byte 1/2 = exponent bytes of the
+// pair), 0x0C = zero byte.  A BF16 pair [raw_j | e1][raw_j+1 | e2] (j = 0 or 2 inside the raw word):
+constexpr uint32_t kSelPair0 = 0x06010500u;   // weights 0,1 of a raw word
+constexpr uint32_t kSelPair2 = 0x06030502u;   // weights 2,3
+// fp32 weights [0][0][raw_j][e_b] for the fp32-activation path
+__device__ __forceinline__ constexpr uint32_t sel_f32(uint32_t j, uint32_t eb) { return (eb << 24) | (j << 16) | 0x0C0Cu; }
+
+// ---- half-wave (32-lane) cross-lane operations ----
+__device__ __forceinline__ uint32_t half_scan_incl(uint32_t v, uint32_t L) {
+#pragma unroll
+    for (int o = 1; o < 32; o <<= 1) {
+        uint32_t y = __shfl_up(v, o, 32);
+        if (L >= (uint32_t)o) v += y;
+    }
+    return v;
+}
+__device__ __forceinline__ float xor_f(float v, int m) { return __shfl_xor(v, m, 32); }
+
+// Transposed reduction of 8 row sums over the 32 lanes of a half: afterwards lane L with (L & 3) == 0 holds the sum
+// of row L >> 2 (9 exchanges instead of 8 x 5).
+__device__ __forceinline__ float reduce8_transposed(float acc[8], uint32_t L) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const bool up = L & 16;
+        float send = up ? acc[i] : acc[i + 4], keep = up ? acc[i + 4] : acc[i];
+        acc[i] = keep + xor_f(send, 16);
+    }
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const bool up = L & 8;
+        float send = up ? acc[i] : acc[i + 2], keep = up ? acc[i + 2] : acc[i];
+        acc[i] = keep + xor_f(send, 8);
+    }
+    const bool up = L & 4;
+    float send = up ? acc[0] : acc[1], keep = up ? acc[1] : acc[0];
+    float v = keep + xor_f(send, 4);
+    v += xor_f(v, 2);
+    v += xor_f(v, 1);
+    return v;
+}
+
+// ---- decode table in LDS ----
+// The stored 4096-word LUT is re-encoded once per workgroup:
+//   two complete codes:  byte 0 = 32 - c (c = bits of both codes, 4..12), bytes 1/2 = exponent bytes, byte 3 = 0
+//   anything else:       bit 31 set (slow path)
+// Byte 0 is then directly the v_alignbit shift that advances the window by c, and two entries added give the
+// shift for both pairs in their low 5 bits and 64 - c1 - c2 in byte 0.
+struct LutLds {
+    uint32_t tab[kLutWords];
+    uint8_t eor[16];            // exp_of_rank, read back from the table (the slow path's rank -> byte map)
+};
+
+__device__ __forceinline__ void stage_lut(LutLds &s, const uint32_t *__restrict__ lut) {
+    const uint32_t tid = threadIdx.x, nth = blockDim.x;
+    for (uint32_t i = tid; i < kLutWords / 4; i += nth) {
+        uint4 v = ((const uint4 *)lut)[i];
+        uint32_t e[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int k = 0; k < 4; k++)
+            e[k] = (e[k] & kFlag) ? (e[k] | 0x80000000u) : ((e[k] & 0xFFFFFF00u) | ((32u - (e[k] & 0xFFu)) & 31u));
+        ((uint4 *)s.tab)[i] = make_uint4(e[0], e[1], e[2], e[3]);
+    }
+    if (tid < 16) {
+        uint32_t e, sh = 8;
+        if (tid < 11) e = lut[1u << (kPeek - 1 - tid)];          // pattern "r zeros, one, sign 0"
+        else if (tid < 15) { e = lut[(tid - 11) >> 1]; sh = (tid & 1) ? 8 : 16; }   // 11,13: byte 1; 12,14: byte 2
+        else e = 0;
+        s.eor[tid] = (uint8_t)((e >> sh) & 0x7Fu);
+    }
+    __syncthreads();
+}
+
+__device__ __forceinline__ uint32_t lds_entry(const LutLds &s, uint32_t byte_off) {
+    return *(const uint32_t *)((const char *)s.tab + byte_off);
+}
+
+// ---- prefix-code window ----
+// hi:lo is a 64-bit MSB-first window holding `avail` valid bits (>= 32 between steps); w is the next stream word,
+// already loaded, at byte offset `off` of `data`.  Bits below the valid ones are zero.
+template <int ELEM>
+struct Window {
+    const uint8_t *data;
+    uint32_t hi, lo, w, avail, off;
+
+    __device__ __forceinline__ uint32_t word(uint32_t o) const { return *(const uint32_t *)(data + o); }
+
+    __device__ __forceinline__ void init(const uint8_t *d, uint32_t o) {
+        data = d;
+        hi = word(o); lo = word(o + 4); w = word(o + 8);
+        off = o + 8; avail = 64;
+    }
+
+    // advance by 1 <= c <= 24 bits and refill (slow path)
+    __device__ __forceinline__ void consume(uint32_t c) {
+        hi = __builtin_amdgcn_alignbit(hi, lo, 32u - c);
+        lo <<= c;
+        avail -= c;
+        if (avail < 32) {
+            hi |= w >> avail;
+            lo |= w << (32u - avail);
+            avail += 32;
+            off += 4;
+            w = word(off);
+        }
+    }
+
+    // one code by counting leading zeros: rank r < max -> r zeros, one, sign; BF16 escape -> 15 zeros, one, byte
+    __device__ __forceinline__ uint32_t one_code(const LutLds &s) {
+        uint32_t u = __clz((int)hi);
+        if (ELEM == kElemFp8 || u < kMaxRankBf16) {
+            u = u < 15u ? u : 15u;
+            const uint32_t b = (((hi >> (30u - u)) & 1u) << 7) | s.eor[u];
+            consume(u + 2);
+            return b;
+        }
+        consume(16);
+        const uint32_t b = hi >> 24;
+        consume(8);
+        return b;
+    }
+
+    // Four codes = two pairs.  Returns e1 with the exponent bytes of weights 0,1 in bytes 1,2 and e2 with those of
+    // weights 2,3.  Fast path: two table reads (the second at the window shifted by the first pair), one window
+    // advance for both pairs, at most one refill.
+    __device__ __forceinline__ void quad(const LutLds &s, uint32_t &e1, uint32_t &e2) {
+        e1 = lds_entry(s, (hi >> 18) & 0x3FFCu);
+        const uint32_t t = __builtin_amdgcn_alignbit(hi, 0u, e1);      // hi << c1
+        e2 = lds_entry(s, (t >> 18) & 0x3FFCu);
+        if ((int)(e1 | e2) < 0) {
+            const uint32_t b0 = one_code(s), b1 = one_code(s), b2 = one_code(s), b3 = one_code(s);
+            e1 = (b0 << 8) | (b1 << 16);
+            e2 = (b2 << 8) | (b3 << 16);
+        } else {
+            const uint32_t d = e1 + e2;                                // low 5 bits: 32 - (c1 + c2) mod 32
+            uint32_t nhi = __builtin_amdgcn_alignbit(hi, lo, d);
+            uint32_t nlo = __builtin_amdgcn_alignbit(lo, 0u, d);
+            const uint32_t tt = avail + (d & 0xFFu);                  // avail - c1 - c2 + 64, in [72, 128)
+            const bool need = tt < 96;                                 // fewer than 32 valid bits left
+            const uint32_t ins = need ? w : 0u;
+            nhi |= __builtin_amdgcn_alignbit(0u, ins, tt);             // ins >> avail'
+            nlo |= __builtin_amdgcn_alignbit(ins, 0u, tt);             // ins << (32 - avail')
+            hi = nhi; lo = nlo;
+            avail = (tt & ~0x60u) | 0x20u;                             // avail' (+32 if refilled)
+            if (need) { off += 4; w = word(off); }
+        }
+    }
+
+    // skip four codes (gather: rows in front of the wanted one)
+    __device__ __forceinline__ void skip_quad(const LutLds &s) { uint32_t a, b; quad(s, a, b); }
+};
+
+// lane stream start of block b inside `data`: bases[b] + 4 * (words of the lanes before L)
+__device__ __forceinline__ uint32_t lane_start(const uint32_t *__restrict__ bases, const uint8_t *__restrict__ hdr,
+                                               uint32_t b, uint32_t L) {
+    const uint32_t n = hdr[(uint64_t)b * kHdrBytes + L];
+    const uint32_t incl = half_scan_incl(n, L);
+    return bases[b] + 4u * (incl - n);
+}
+
+// raw bytes of a lane's 16 weights for the PRMT stage: word k holds weights 4k..4k+3 (fp8: nibble << 4)
+__device__ __forceinline__ uint4 expand_nibbles(uint2 c) {
+    return make_uint4((c.x << 4) & 0xF0F0F0F0u, c.x & 0xF0F0F0F0u, (c.y << 4) & 0xF0F0F0F0u, c.y & 0xF0F0F0F0u);
+}
+__device__ __forceinline__ uint32_t u4_get(const uint4 &v, int k) { return k == 0 ? v.x : k == 1 ? v.y : k == 2 ? v.z : v.w; }
+
+// Launch arguments shared by the block kernels.
+struct BlockArgs {
+    const uint8_t *data;
+    const uint32_t *bases;
+    const uint8_t *hdr;
+    const uint32_t *lut;
+    const uint8_t *low;
+    const void *x;          // fp32 or BF16 activations
+    const uint16_t *bias;   // BF16 [M] or null
+    const float *scale;     // fp32 [M] or null
+    void *out;              // token: BF16 y [M]; fp32 path: y [M]; dequant: BF16 [M x K16]
+    uint32_t M, K;
+    uint32_t G;             // row groups per workgroup
+};
+
+struct GatherArgs {
+    const uint8_t *data;
+    const uint32_t *bases;
+    const uint8_t *hdr;
+    const uint32_t *lut;
+    const uint8_t *low;
+    const int64_t *ids;
+    uint32_t n_ids;
+    uint16_t *out;
+    uint32_t M, K;
+};
+
+enum Mode { kToken = 0, kDequant = 1, kF32 = 2 };
+
+// Workgroup epilogue of the token / fp32 paths: rows of the tile summed over the column blocks (ascending),
+// times scale, plus bias, rounded to BF16 (token) or written as fp32.
+template <int MODE>
+__device__ __forceinline__ void finish_rows(const BlockArgs &a, const float *part, uint32_t row0, uint32_t nrows, uint32_t CB) {
+    __syncthreads();
+    for (uint32_t i = threadIdx.x; i < nrows; i += blockDim.x) {
+        const uint32_t row = row0 + i;
+        if (row >= a.M) break;
+        float v = 0.f;
+        for (uint32_t cb = 0; cb < CB; cb++) v += part[i * CB + cb];
+        if (MODE == kToken) {
+            if (a.scale) v *= a.scale[row];
+            if (a.bias) v += __uint_as_float((uint32_t)a.bias[row] << 16);
+            ((uint16_t *)a.out)[row] = (uint16_t)f32_to_bf16_rne(v);
+        } else {
+            ((float *)a.out)[row] = v;
+        }
+    }
+}
+
+}  // namespace nwc

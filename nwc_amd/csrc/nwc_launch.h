@@ -1,0 +1,18 @@
+// nwc_launch.h -- launch plans and the launchers each kernel file exports to the C ABI layer (abi.cpp).
+#pragma once
+#include "nwc_device.h"
+
+namespace nwc {
+
+struct LaunchPlan {
+    int layout;
+    uint32_t grid, threads, lds, G;
+};
+
+int launch_prefix(const LaunchPlan &p, int elem_t, int mode, bool xbf16, const BlockArgs &a, hipStream_t st);
+int launch_fixed(const LaunchPlan &p, int elem_t, int mode, bool xbf16, const BlockArgs &a, hipStream_t st);
+int launch_gather_prefix(int layout, int elem_t, const GatherArgs &a, hipStream_t st);
+int launch_gather_fixed(int elem_t, const GatherArgs &a, hipStream_t st);
+int launch_ref_fp8(const uint8_t *w, const float *scale, const float *x, uint16_t *y, uint32_t M, uint32_t K, hipStream_t st);
+
+}  // namespace nwc

@@ -1,0 +1,143 @@
+"""GPU parity of the gfx950 kernels against the oracle and against closed forms, through the C ABI (nwc_amd).
+
+Bars:
+  * decoded weights bit-exact: dequant and gather equal the original BF16 / fp8 values and the oracle's decode;
+  * fp32 path (nwc_matvec): |y - y64| <= 1e-3 |y64| + 1e-5 * (sigma / 0.02), y64 = float64 matvec on the decoded
+    weights (sigma = weight scale of the test matrix; 1e-5 absolute at the north star's N(0, 0.02^2));
+  * token path (BF16 out): |y - y64| <= 2^-8 |y64| + the same absolute term, i.e. within one BF16 ulp of the exact
+    result (BF16 rounding alone is up to 2^-9 relative, so 1e-3 cannot be applied to the rounded output).
+Shapes and stressors follow the reference tests (tests/test_format_cpu.py:127-131, test_k.py:10-11, test_fp8.py:19,44).
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from tests.helpers import bf16_matrix, bits16, fp8_source, oracle_encoding, ref_matvec64
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = [(8, 512, 0.02), (13, 40, 0.02), (3, 4097, 0.02), (100, 1000, 1.0), (64, 2048, 0.02), (17, 520, 0.02),
+          (1001, 1000, 0.02), (8, 16, 0.02), (1, 1, 0.02)]
+FP8_SHAPES = [(8, 512), (13, 40), (3, 4097), (1001, 1000), (2560, 4096)]
+LAYOUTS = [0, 1, 2]
+
+
+def _nwc():
+    from nwc_amd.nwc_torch import NWCWeight, ref_fp8_matvec, quantize_fp8
+    return NWCWeight, ref_fp8_matvec, quantize_fp8
+
+
+def _check_f32(y, y64, sigma):
+    err = np.abs(np.asarray(y, np.float64) - y64)
+    tol = 1e-3 * np.abs(y64) + 1e-5 * max(1.0, sigma / 0.02)
+    assert np.all(err <= tol), f"fp32 path: worst excess {np.max(err - tol):.3e}"
+
+
+def _check_bf16(y_bf16, y64, sigma):
+    y = y_bf16.float().cpu().double().numpy()
+    err = np.abs(y - y64)
+    tol = 2.0 ** -8 * np.abs(y64) + 1e-5 * max(1.0, sigma / 0.02)
+    assert np.all(err <= tol), f"token path: worst excess {np.max(err - tol):.3e}"
+
+
+@pytest.mark.parametrize("layout", LAYOUTS)
+@pytest.mark.parametrize("M,K,sigma", SHAPES)
+def test_bf16_all_paths(cuda, layout, M, K, sigma):
+    NWCWeight, _, _ = _nwc()
+    print(f"bf16 layout {layout} {M}x{K}", flush=True)
+    w = bf16_matrix(M, K, seed=M * 7 + K, scale=sigma)
+    c = NWCWeight(w, device="cuda", layout=layout)
+    wb = bits16(w)
+    # decoded weights: bit-exact against the original and against the oracle decoding the same tensors
+    d = c.dequant().cpu()
+    assert torch.equal(d.view(torch.int16), w.view(torch.int16))
+    assert np.array_equal(O.decode(oracle_encoding(c)), wb)
+    # token path with bias
+    g = torch.Generator().manual_seed(1)
+    x = torch.randn(K, generator=g).to(torch.bfloat16)
+    bias = (torch.rand(M, generator=g) - 0.5).to(torch.bfloat16)
+    y = c.linear_bf16(x.cuda(), bias.cuda())
+    y64 = ref_matvec64(wb, x.float().numpy(), bias_bits=bits16(bias))
+    _check_bf16(y, y64, sigma)
+    # token path with fp32 activations (reference ABI for layout 0) and without bias
+    y2 = c.linear_bf16(x.float().cuda(), None)
+    _check_bf16(y2, ref_matvec64(wb, x.float().numpy()), sigma)
+    # fp32 path with non-BF16 activations
+    xf = torch.rand(K, generator=g) - 0.5
+    y32 = c.matvec(xf.cuda()).cpu().numpy()
+    _check_f32(y32, ref_matvec64(wb, xf.numpy()), sigma)
+    # gather, including the first, last and middle rows
+    ids = torch.cat([torch.tensor([0, M - 1, M // 2]), torch.randint(0, M, (13,), generator=g)])
+    rows = c.gather(ids.cuda()).cpu()
+    assert torch.equal(rows.view(torch.int16), w[ids].view(torch.int16))
+
+
+@pytest.mark.parametrize("layout", LAYOUTS)
+@pytest.mark.parametrize("M,K", FP8_SHAPES)
+def test_fp8_all_paths(cuda, layout, M, K):
+    NWCWeight, ref_fp8_matvec, quantize_fp8 = _nwc()
+    print(f"fp8 layout {layout} {M}x{K}", flush=True)
+    w = fp8_source(M, K, seed=M)
+    q, scale = quantize_fp8(w)
+    ref_vals = q.to(torch.bfloat16)                     # unscaled fp8 values, exact in BF16
+    c = NWCWeight(w, device="cuda", elem="fp8", layout=layout)
+    assert torch.equal(c.dequant().cpu().view(torch.int16), ref_vals.view(torch.int16))
+    q2, s2 = c.dequant_fp8()
+    assert torch.equal(q2.cpu().view(torch.uint8), q.view(torch.uint8))
+    assert torch.equal(s2.cpu(), scale)
+    assert np.array_equal(O.decode(oracle_encoding(c)), bits16(ref_vals))
+    g = torch.Generator().manual_seed(2)
+    x = torch.randn(K, generator=g)
+    vb = bits16(ref_vals)
+    y64 = ref_matvec64(vb, x.to(torch.bfloat16).float().numpy(), scale=scale.numpy())
+    _check_bf16(c.linear_bf16(x.to(torch.bfloat16).cuda(), None), y64, 0.02)
+    y32 = c.matvec(x.cuda()).cpu().numpy()
+    _check_f32(y32, ref_matvec64(vb, x.numpy(), scale=scale.numpy()), 0.02)
+    ids = torch.randint(0, M, (7,), generator=g)
+    assert torch.equal(c.gather(ids.cuda()).cpu().view(torch.int16), ref_vals[ids].view(torch.int16))
+    yr = ref_fp8_matvec(q.cuda().contiguous(), scale.cuda(), x.cuda())
+    _check_bf16(yr, ref_matvec64(vb, x.numpy(), scale=scale.numpy()), 0.02)
+
+
+def test_fp8_nan_rejected():
+    NWCWeight, _, _ = _nwc()
+    bad = torch.full((8, 512), float("nan")).to(torch.float8_e4m3fn)
+    with pytest.raises(ValueError):
+        NWCWeight(bad, device="cpu", elem="fp8", scale=torch.ones(8))
+
+
+def test_fp8_hardware_conversion_exhaustive(cuda):
+    """The native fp8 baseline converts with v_cvt_pk_f32_fp8; every finite e4m3fn code must give its exact value
+    (closed form from the definition, oracle or_e4m3_to_f32)."""
+    _, ref_fp8_matvec, _ = _nwc()
+    codes = np.array([c for c in range(256) if (c & 0x7F) != 0x7F], np.uint8)
+    M, K = codes.size, 32
+    w = np.zeros((M, K), np.uint8)
+    w[:, 5] = codes
+    x = torch.zeros(K)
+    x[5] = 1.0
+    y = ref_fp8_matvec(torch.from_numpy(w).cuda().view(torch.float8_e4m3fn), torch.ones(M).cuda(), x.cuda()).cpu()
+    exact = O.e4m3_to_f32(codes)
+    # values, not bits: a matvec returns +0 for the -0 code (0x80)
+    assert np.array_equal(y.float().numpy(), exact)
+
+
+@pytest.mark.parametrize("layout", LAYOUTS)
+def test_full_size_qwen3_4b_gate_up(cuda, layout):
+    """BASELINE config 3's largest matrix at its real shape: dequant bit-exact and the token path against a torch
+    fp32 matvec on the GPU (size-independent checks; the oracle covers the small shapes)."""
+    NWCWeight, _, _ = _nwc()
+    M, K = 19456, 2560
+    print(f"full size layout {layout}", flush=True)
+    w = bf16_matrix(M, K, seed=11, escapes=False)
+    c = NWCWeight(w, device="cuda", layout=layout)
+    wc = w.cuda()
+    assert torch.equal(c.dequant().view(torch.int16), wc.view(torch.int16))
+    x = torch.randn(K, generator=torch.Generator().manual_seed(3)).to(torch.bfloat16).cuda()
+    y = c.linear_bf16(x, None).double().cpu().numpy()
+    y64 = (wc.double() @ x.double()).cpu().numpy()
+    err = np.abs(y - y64)
+    assert np.all(err <= 2.0 ** -8 * np.abs(y64) + 1e-5)
+    y32 = c.matvec(x.float()).double().cpu().numpy()
+    assert np.all(np.abs(y32 - y64) <= 1e-3 * np.abs(y64) + 1e-5)
