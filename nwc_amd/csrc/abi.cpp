@@ -3,6 +3,7 @@
 #include "nwc_launch.h"
 #include "nwc_ops.h"
 
+#include <algorithm>
 #include <atomic>
 
 using namespace nwc;
@@ -28,24 +29,41 @@ bool shape_ok(uint64_t n, uint32_t block, uint32_t K, int elem) {
            elem_layout(elem) <= 2 && (elem & ~0xFF) == 0;
 }
 
-// Workgroup tile = G whole row groups.  Prefer at least two workgroups per CU (small matrices spread over the
-// whole chip), at most 32 blocks (16 waves) per workgroup, and an even block count so both halves of every wave
-// have a block.
-LaunchPlan plan_blocks(const Shape &f, int layout, int mode, int ncu) {
-    LaunchPlan p{};
+// LDS words per half-wave for a staged block: an 8 x 512 block of N(0, 0.02^2) BF16 needs ~370 words, real model
+// weights (2.85-2.99 code bits per weight) ~405; a 16 x 512 block twice that.  Larger blocks decode from global
+// memory instead.
+constexpr uint32_t kSlotWords0 = 480, kSlotWords1 = 960;
+constexpr uint32_t kDynLdsBudget = 48u * 1024u;       // dynamic LDS per workgroup next to the 16 KB decode table
+
+uint32_t slot_words_for(int layout) { return layout == 0 ? kSlotWords0 : layout == 1 ? kSlotWords1 : 0u; }
+
+// Workgroup tile = G whole row groups, one block per half-wave where the LDS budget allows.  Prefer at least two
+// workgroups per CU (small matrices spread over the whole chip), at most 32 blocks (16 waves) per workgroup, and an
+// even block count so both halves of every wave have a block.
+bool plan_blocks(const Shape &f, int layout, int mode, int ncu, LaunchPlan &p) {
+    p = LaunchPlan{};
     p.layout = layout;
-    const uint32_t CB = f.CB, groups = f.groups();
+    const uint32_t CB = f.CB, groups = f.groups(), slot = slot_words_for(layout);
     uint32_t G = CB >= 32 ? 1u : 32u / CB;
     while (G > 1 && (groups + G - 1) / G < 2u * (uint32_t)ncu) G--;
     if (G > 1 && ((G * CB) & 1u)) G--;
     if (G > groups) G = groups;
     if (G == 0) G = 1;
-    const uint32_t blocks = G * CB;
+    auto lds_of = [&](uint32_t g, uint32_t halves) {
+        return halves * slot * 4u + (mode == kDequant ? 0u : g * f.rows * CB * 4u);
+    };
+    uint32_t halves = std::min(32u, (G * CB + 1) & ~1u);
+    while (G > 1 && lds_of(G, halves) > kDynLdsBudget) {
+        G--;
+        halves = std::min(32u, (G * CB + 1) & ~1u);
+    }
+    while (halves > 2 && lds_of(G, halves) > kDynLdsBudget) halves -= 2;   // several blocks per half-wave
+    if (lds_of(G, halves) > kDynLdsBudget) return false;                     // K beyond ~190k columns
     p.G = G;
-    p.threads = 64u * std::min(16u, (blocks + 1) / 2);
+    p.threads = 32u * halves;
     p.grid = (groups + G - 1) / G;
-    p.lds = mode == kDequant ? 0u : G * f.rows * CB * 4u;
-    return p;
+    p.lds = lds_of(G, halves);
+    return true;
 }
 
 int run_blocks(int mode, bool xbf16, hipStream_t st, const uint8_t *data, const uint32_t *bases, const uint8_t *hdr,
@@ -55,9 +73,9 @@ int run_blocks(int mode, bool xbf16, hipStream_t st, const uint8_t *data, const 
     if (ncu <= 0) return (int)hipErrorNoDevice;
     const int layout = elem_layout(elem), t = elem_type(elem);
     const Shape f((uint32_t)(n / K), K, layout);
-    const LaunchPlan p = plan_blocks(f, layout, mode, ncu);
-    if (p.lds > 48u * 1024u) return -1;        // K beyond what one workgroup's partial sums fit (K > ~98k columns)
-    BlockArgs a{data, bases, hdr, tab, low, x, bias, scale, out, f.M, f.K, p.G};
+    LaunchPlan p;
+    if (!plan_blocks(f, layout, mode, ncu, p)) return -1;
+    BlockArgs a{data, bases, hdr, tab, low, x, bias, scale, out, f.M, f.K, p.G, slot_words_for(layout)};
     return layout == 2 ? launch_fixed(p, t, mode, xbf16, a, st) : launch_prefix(p, t, mode, xbf16, a, st);
 }
 
@@ -99,7 +117,7 @@ extern "C" int nwc_gather(void *stream, const uint8_t *data, const uint32_t *bas
     if (!shape_ok(n, block, K, elem)) return -1;
     if (n_ids == 0) return 0;
     if (current_cus() <= 0) return (int)hipErrorNoDevice;
-    GatherArgs a{data, bases, hdr, tab, low, ids, n_ids, out, (uint32_t)(n / K), K};
+    GatherArgs a{data, bases, hdr, tab, low, ids, n_ids, out, (uint32_t)(n / K), K, slot_words_for(elem_layout(elem))};
     const int layout = elem_layout(elem), t = elem_type(elem);
     return layout == 2 ? launch_gather_fixed(t, a, (hipStream_t)stream) : launch_gather_prefix(layout, t, a, (hipStream_t)stream);
 }

@@ -114,19 +114,19 @@ __device__ __forceinline__ uint32_t lds_entry(const LutLds &s, uint32_t byte_off
 }
 
 // ---- prefix-code window ----
-// hi:lo is a 64-bit MSB-first window holding `avail` valid bits (>= 32 between steps); w is the next stream word,
-// already loaded, at byte offset `off` of `data`.  Bits below the valid ones are zero.
-template <int ELEM>
+// hi:lo is a 64-bit MSB-first window holding `avail` valid bits (>= 32 between steps); w is the next stream word and
+// wn the one after it, both already read; p points at wn.  Bits below the valid ones are zero.  P is the word
+// pointer type: an LDS slot (the block's streams staged once) or global memory (fallback).  The fast path reads
+// wn for the next step unconditionally, so no step waits for its own refill read.
+template <int ELEM, typename P>
 struct Window {
-    const uint8_t *data;
-    uint32_t hi, lo, w, avail, off;
+    P p;
+    uint32_t hi, lo, w, wn, avail;
 
-    __device__ __forceinline__ uint32_t word(uint32_t o) const { return *(const uint32_t *)(data + o); }
-
-    __device__ __forceinline__ void init(const uint8_t *d, uint32_t o) {
-        data = d;
-        hi = word(o); lo = word(o + 4); w = word(o + 8);
-        off = o + 8; avail = 64;
+    __device__ __forceinline__ void init(P lane_words) {
+        hi = lane_words[0]; lo = lane_words[1]; w = lane_words[2]; wn = lane_words[3];
+        p = lane_words + 3;
+        avail = 64;
     }
 
     // advance by 1 <= c <= 24 bits and refill (slow path)
@@ -138,8 +138,8 @@ struct Window {
             hi |= w >> avail;
             lo |= w << (32u - avail);
             avail += 32;
-            off += 4;
-            w = word(off);
+            w = wn;
+            wn = *++p;
         }
     }
 
@@ -166,9 +166,11 @@ struct Window {
         const uint32_t t = __builtin_amdgcn_alignbit(hi, 0u, e1);      // hi << c1
         e2 = lds_entry(s, (t >> 18) & 0x3FFCu);
         if ((int)(e1 | e2) < 0) {
-            const uint32_t b0 = one_code(s), b1 = one_code(s), b2 = one_code(s), b3 = one_code(s);
-            e1 = (b0 << 8) | (b1 << 16);
-            e2 = (b2 << 8) | (b3 << 16);
+            uint32_t bytes = 0;                                        // b3 b2 b1 b0 after four codes
+#pragma unroll 1
+            for (int k = 0; k < 4; k++) bytes = (bytes >> 8) | (one_code(s) << 24);
+            e1 = (bytes << 8) & 0x00FFFF00u;
+            e2 = (bytes >> 8) & 0x00FFFF00u;
         } else {
             const uint32_t d = e1 + e2;                                // low 5 bits: 32 - (c1 + c2) mod 32
             uint32_t nhi = __builtin_amdgcn_alignbit(hi, lo, d);
@@ -180,7 +182,9 @@ struct Window {
             nlo |= __builtin_amdgcn_alignbit(ins, 0u, tt);             // ins << (32 - avail')
             hi = nhi; lo = nlo;
             avail = (tt & ~0x60u) | 0x20u;                             // avail' (+32 if refilled)
-            if (need) { off += 4; w = word(off); }
+            w = need ? wn : w;
+            p += need ? 1 : 0;
+            wn = *p;                                                   // used from the next step on
         }
     }
 
@@ -188,12 +192,29 @@ struct Window {
     __device__ __forceinline__ void skip_quad(const LutLds &s) { uint32_t a, b; quad(s, a, b); }
 };
 
-// lane stream start of block b inside `data`: bases[b] + 4 * (words of the lanes before L)
-__device__ __forceinline__ uint32_t lane_start(const uint32_t *__restrict__ bases, const uint8_t *__restrict__ hdr,
-                                               uint32_t b, uint32_t L) {
-    const uint32_t n = hdr[(uint64_t)b * kHdrBytes + L];
-    const uint32_t incl = half_scan_incl(n, L);
-    return bases[b] + 4u * (incl - n);
+// Per-block lane offsets: n = words of lane L, start = words of the lanes before it, total = words of the block.
+struct LaneSpan { uint32_t n, start, total; };
+__device__ __forceinline__ LaneSpan lane_span(const uint8_t *__restrict__ hdr, uint32_t b, uint32_t L) {
+    LaneSpan r;
+    r.n = hdr[(uint64_t)b * kHdrBytes + L];
+    const uint32_t incl = half_scan_incl(r.n, L);
+    r.start = incl - r.n;
+    r.total = __shfl(incl, 31, 32);
+    return r;
+}
+
+// Copies the 32 lane streams of a block (plus the window's read-ahead of two words) into the half-wave's LDS slot with
+// 16-byte loads.  `sh` returns the word offset of the block inside the slot (bases[] are 8-byte aligned, the copy
+// 16-byte aligned).  False when the block does not fit; the caller then decodes from global memory.
+__device__ __forceinline__ bool stage_block(uint32_t *slot, uint32_t slot_words, const uint8_t *__restrict__ data,
+                                            uint32_t base, uint32_t total, uint32_t L, uint32_t &sh) {
+    const uint32_t a16 = base & ~15u;
+    sh = (base & 15u) >> 2;
+    const uint32_t need = sh + total + 3;
+    if (need > slot_words) return false;
+    for (uint32_t i = L * 4; i < need; i += 128) *(uint4 *)(slot + i) = *(const uint4 *)(data + a16 + 4u * i);
+    __builtin_amdgcn_wave_barrier();
+    return true;
 }
 
 // raw bytes of a lane's 16 weights for the PRMT stage: word k holds weights 4k..4k+3 (fp8: nibble << 4)
@@ -215,6 +236,7 @@ struct BlockArgs {
     void *out;              // token: BF16 y [M]; fp32 path: y [M]; dequant: BF16 [M x K16]
     uint32_t M, K;
     uint32_t G;             // row groups per workgroup
+    uint32_t slot_words;    // LDS words per half-wave for a staged block (layouts 0/1)
 };
 
 struct GatherArgs {
@@ -227,6 +249,7 @@ struct GatherArgs {
     uint32_t n_ids;
     uint16_t *out;
     uint32_t M, K;
+    uint32_t slot_words;
 };
 
 enum Mode { kToken = 0, kDequant = 1, kF32 = 2 };
