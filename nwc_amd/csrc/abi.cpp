@@ -37,10 +37,49 @@ constexpr uint32_t kDynLdsBudget = 48u * 1024u;       // dynamic LDS per workgro
 
 uint32_t slot_words_for(int layout) { return layout == 0 ? kSlotWords0 : layout == 1 ? kSlotWords1 : 0u; }
 
-// Workgroup tile = G whole row groups, one block per half-wave where the LDS budget allows.  Prefer at least two
-// workgroups per CU (small matrices spread over the whole chip), at most 32 blocks (16 waves) per workgroup, and an
-// even block count so both halves of every wave have a block.
+// Layout 0: a workgroup owns G whole row groups, with G chosen so the grid is one residency round at two workgroups
+// per CU.  Tiles of at most 20 blocks get one half-wave per block (k_layout0); larger tiles are spread evenly over at
+// most 16 half-waves that each decode several blocks through two LDS slots (k_layout0_pipe).
+constexpr uint32_t kDynLdsPipe = 62u * 1024u;         // two such workgroups per CU next to their decode tables
+
+bool plan_layout0(const Shape &f, int mode, int ncu, LaunchPlan &p) {
+    p = LaunchPlan{};
+    p.layout = 0;
+    const uint32_t CB = f.CB, groups = f.groups(), slot = kSlotWords0;
+    const uint32_t part = mode == kDequant ? 0u : kRows0 * CB * 4u;     // row-sum bytes per row group
+    uint32_t G = std::max(1u, (groups + 2u * (uint32_t)ncu - 1u) / (2u * (uint32_t)ncu));
+    for (;; G--) {
+        const uint32_t blocks = G * CB;
+        uint32_t halves, lds;
+        bool pipe;
+        if (blocks <= 20) {
+            halves = (blocks + 1u) & ~1u;
+            lds = halves * slot * 4u + G * part;
+            pipe = false;
+        } else {
+            const uint32_t rounds = (blocks + 15u) / 16u;
+            halves = ((blocks + rounds - 1u) / rounds + 1u) & ~1u;
+            while (halves > 2 && halves * 2u * slot * 4u + G * part > kDynLdsPipe) halves -= 2;
+            lds = halves * 2u * slot * 4u + G * part;
+            pipe = true;
+        }
+        if (lds <= (pipe ? kDynLdsPipe : kDynLdsBudget)) {
+            p.pipe = pipe;
+            p.G = G;
+            p.threads = 32u * halves;
+            p.grid = (groups + G - 1u) / G;
+            p.lds = lds;
+            return true;
+        }
+        if (G == 1) return false;                            // K beyond ~190k columns
+    }
+}
+
+// Layouts 1/2: workgroup tile = G whole row groups, one block per half-wave where the LDS budget allows.  Prefer at
+// least two workgroups per CU (small matrices spread over the whole chip), at most 32 blocks (16 waves) per
+// workgroup, and an even block count so both halves of every wave have a block.
 bool plan_blocks(const Shape &f, int layout, int mode, int ncu, LaunchPlan &p) {
+    if (layout == 0) return plan_layout0(f, mode, ncu, p);
     p = LaunchPlan{};
     p.layout = layout;
     const uint32_t CB = f.CB, groups = f.groups(), slot = slot_words_for(layout);

@@ -190,8 +190,8 @@ __global__ void __launch_bounds__(1024) k_layout2(BlockArgs a) {
         }
         if (MODE != kDequant) {
             accA += eA; accB += eB;
-            accA += xor_f(accA, 1); accA += xor_f(accA, 2);
-            accB += xor_f(accB, 1); accB += xor_f(accB, 2);
+            accA += xor_f<1>(accA); accA += xor_f<2>(accA);
+            accB += xor_f<1>(accB); accB += xor_f<2>(accB);
             if (q == 0) {
                 part[(g * kRows12 + r) * f.CB + cb] = accA;
                 part[(g * kRows12 + r + 8) * f.CB + cb] = accB;

@@ -45,15 +45,22 @@ constexpr uint32_t kSelPair2 = 0x06030502u;   // weights 2,3
 __device__ __forceinline__ constexpr uint32_t sel_f32(uint32_t j, uint32_t eb) { return (eb << 24) | (j << 16) | 0x0C0Cu; }
 
 // ---- half-wave (32-lane) cross-lane operations ----
+// Inclusive prefix sum inside each 32-lane half: DPP row shifts within 16-lane rows, then row 1 (3) adds the last
+// lane of row 0 (2).
 __device__ __forceinline__ uint32_t half_scan_incl(uint32_t v, uint32_t L) {
-#pragma unroll
-    for (int o = 1; o < 32; o <<= 1) {
-        uint32_t y = __shfl_up(v, o, 32);
-        if (L >= (uint32_t)o) v += y;
-    }
+    (void)L;
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x111, 0xF, 0xF, false);   // row_shr:1
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x112, 0xF, 0xF, false);   // row_shr:2
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x114, 0xF, 0xF, false);   // row_shr:4
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x118, 0xF, 0xF, false);   // row_shr:8
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x142, 0xA, 0xF, false);   // row_bcast:15 into rows 1, 3
     return v;
 }
-__device__ __forceinline__ float xor_f(float v, int m) { return __shfl_xor(v, m, 32); }
+// value of lane `m ^ L` inside the 32-lane half (ds_swizzle bit mode: and 0x1F, or 0, xor m)
+template <int M>
+__device__ __forceinline__ float xor_f(float v) {
+    return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), (M << 10) | 0x1F));
+}
 
 // Transposed reduction of 8 row sums over the 32 lanes of a half: afterwards lane L with (L & 3) == 0 holds the sum
 // of row L >> 2 (9 exchanges instead of 8 x 5).
@@ -62,19 +69,19 @@ __device__ __forceinline__ float reduce8_transposed(float acc[8], uint32_t L) {
     for (int i = 0; i < 4; i++) {
         const bool up = L & 16;
         float send = up ? acc[i] : acc[i + 4], keep = up ? acc[i + 4] : acc[i];
-        acc[i] = keep + xor_f(send, 16);
+        acc[i] = keep + xor_f<16>(send);
     }
 #pragma unroll
     for (int i = 0; i < 2; i++) {
         const bool up = L & 8;
         float send = up ? acc[i] : acc[i + 2], keep = up ? acc[i + 2] : acc[i];
-        acc[i] = keep + xor_f(send, 8);
+        acc[i] = keep + xor_f<8>(send);
     }
     const bool up = L & 4;
     float send = up ? acc[0] : acc[1], keep = up ? acc[1] : acc[0];
-    float v = keep + xor_f(send, 4);
-    v += xor_f(v, 2);
-    v += xor_f(v, 1);
+    float v = keep + xor_f<4>(send);
+    v += xor_f<2>(v);
+    v += xor_f<1>(v);
     return v;
 }
 

@@ -6,6 +6,7 @@ namespace nwc {
 
 struct LaunchPlan {
     int layout;
+    bool pipe;              // layout 0: two LDS slots per half-wave, next block prefetched (k_layout0_pipe)
     uint32_t grid, threads, lds, G;
 };
 
