@@ -97,58 +97,144 @@ __device__ __forceinline__ void store_row0(const BlockArgs &a, const Shape &f, u
     }
 }
 
-// The eight rows of one layout-0 block for one lane, decoded from its LDS slot with all raw-plane rows already
-// requested.  Returns the row sums reduced over the half-wave (lane 4r holds row r) or, for dequantization, stores
-// the rows.  Fully unrolled: every row's raw bytes live in their own registers.
+// ---- workgroup staging of the streams of a run of consecutive blocks ----
+// The blocks of a workgroup's tile are consecutive in `data`, so a round of H blocks (one per half-wave) is one
+// contiguous byte range: [bases[b_lo], bases[b_hi]) -- for the matrix's last block, its base plus four bytes per header
+// word.  All threads copy it into LDS with 16-byte loads; no half-wave needs its own header scan before the copy.
+struct Region {
+    uint32_t lo16, n16;         // 16-byte aligned start (byte offset into data), 16-byte chunks
+};
+
+// One past the last stream byte of the matrix (block nb - 1: its base plus four bytes per header word).
+__device__ __forceinline__ uint32_t matrix_end(const BlockArgs &a, uint32_t nb) {
+    const uint32_t *h = (const uint32_t *)(a.hdr + (uint64_t)(nb - 1u) * kHdrBytes);
+    uint32_t words = 0;
+#pragma unroll
+    for (int i = 0; i < (int)kHdrBytes / 4; i++) words = __builtin_amdgcn_udot4(h[i], 0x01010101u, words, false);
+    return a.bases[nb - 1u] + 4u * words;
+}
+
+// Blocks [b_lo, b_hi) plus the 16 bytes the last lane's window reads past its stream (inside the 64 slack bytes that
+// follow the matrix's last block).
+__device__ __forceinline__ Region region_of(const BlockArgs &a, uint32_t b_lo, uint32_t b_hi, uint32_t nb, uint32_t mend) {
+    const uint32_t s = a.bases[b_lo], e = a.bases[min(b_hi, nb - 1u)];
+    Region r;
+    r.lo16 = s & ~15u;
+    r.n16 = ((b_hi < nb ? e : mend) + 16u - r.lo16 + 15u) >> 4;
+    return r;
+}
+
+// Four 16-byte chunks per thread cover a region buffer of up to 512 words per half-wave.  Lanes past the region
+// re-read its last chunk, so the load count is fixed; native vectors keep the words in registers.
+struct Bulk {
+    u32x4_t v0, v1, v2, v3;
+};
+__device__ __forceinline__ void bulk_issue(Bulk &B, const uint8_t *__restrict__ data, const Region &r, uint32_t tid, uint32_t nth) {
+    const uint8_t *p = data + r.lo16;
+    const uint32_t last = r.n16 - 1u;
+    B.v0 = *(const u32x4_t *)(p + 16u * min(tid, last));
+    B.v1 = *(const u32x4_t *)(p + 16u * min(tid + nth, last));
+    B.v2 = *(const u32x4_t *)(p + 16u * min(tid + 2u * nth, last));
+    B.v3 = *(const u32x4_t *)(p + 16u * min(tid + 3u * nth, last));
+}
+__device__ __forceinline__ void bulk_commit(const Bulk &B, uint32_t *buf, const Region &r, uint32_t tid, uint32_t nth) {
+    if (tid < r.n16) *(u32x4_t *)(buf + 4u * tid) = B.v0;
+    if (tid + nth < r.n16) *(u32x4_t *)(buf + 4u * (tid + nth)) = B.v1;
+    if (tid + 2u * nth < r.n16) *(u32x4_t *)(buf + 4u * (tid + 2u * nth)) = B.v2;
+    if (tid + 3u * nth < r.n16) *(u32x4_t *)(buf + 4u * (tid + 3u * nth)) = B.v3;
+}
+
+// One row of a layout-0 block for one lane (16 weights = four steps of the cursor), dot product with the lane's
+// activations or, for dequantization, the eight BF16 pairs in pw.  A step whose table entries were not both fast in
+// some lane of the wave is redone code by code from its start by the whole wave (0.09% of lane-steps, 5% of
+// wave-steps for N(0, 0.02^2) BF16 at a 12-bit window).
+template <int ELEM, int MODE, bool XBF16>
+__device__ __forceinline__ float row0(Seq<ELEM> &S, const LutLds &s, const uint4 &rw, const XRegs<XBF16> &x, uint32_t pw[8]) {
+    float sum = 0.f;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const int32_t nm0 = S.nm;
+        const uint32_t *wp0 = S.wp;
+        uint32_t e1, e2;
+        S.fast_quad(s, e1, e2);
+        if (__any((int)(e1 | e2) < 0)) {
+            S.nm = nm0;
+            S.wp = wp0;
+            S.reload();
+            S.slow_quad(s, e1, e2);
+        }
+        use_quad<MODE, XBF16>(e1, e2, u4_get(rw, k), k, x, sum, pw);
+        // consume each step's weights before the next decode step (otherwise the compiler sinks every dot product to
+        // the end of the unrolled block and keeps all decoded words live)
+        if (MODE == kDequant) asm volatile("" : "+v"(pw[2 * k]), "+v"(pw[2 * k + 1]));
+        else asm volatile("" : "+v"(sum));
+    }
+    return sum;
+}
+
+// The eight rows of one layout-0 block for one lane, decoded from LDS with all raw-plane rows already requested.
+// Returns the row sums reduced over the half-wave (lane 4r holds row r) or, for dequantization, stores the rows.
 template <int ELEM, int MODE, bool XBF16>
 __device__ __forceinline__ float rows0(const LutLds &s, const uint32_t *words, const BlockArgs &a, const Shape &f,
                                        const XRegs<XBF16> &x, const uint4 raw[8], const Coord0 &c, uint32_t L) {
-    Window<ELEM, const uint32_t *> W;
-    W.init(words);
+    Seq<ELEM> S;
+    S.init(words);
     float acc[8];
 #pragma unroll
     for (int r = 0; r < (int)kRows0; r++) {
-        float sum = 0.f;
         uint32_t pw[8];
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-            uint32_t e1, e2;
-            W.quad(s, e1, e2);
-            use_quad<MODE, XBF16>(e1, e2, u4_get(raw[r], k), k, x, sum, pw);
-            // consume each step's weights before the next decode step (otherwise the compiler sinks every dot
-            // product to the end of the unrolled block and keeps all decoded words live)
-            if (MODE == kDequant) asm volatile("" : "+v"(pw[2 * k]), "+v"(pw[2 * k + 1]));
-            else asm volatile("" : "+v"(sum));
-        }
+        const float sum = row0<ELEM, MODE, XBF16>(S, s, raw[r], x, pw);
         if (MODE == kDequant) store_row0<MODE>(a, f, c.row0 + r, c.col0, c.col_ok, pw);
         else acc[r] = c.col_ok ? sum : 0.f;
     }
     return MODE == kDequant ? 0.f : reduce8_transposed(acc, L);
 }
 
-// The same for a block whose streams do not fit the LDS slot: decoded straight from global memory with a rolled row
-// loop and its own raw loads (compact code; such blocks are rare, e.g. near-uniform exponent distributions).  Lanes
-// past K16 have empty streams; the callers point them at the block's first word, since decoding zero bits walks up
-// to 96 words (all escapes), which stays inside a block too large for the slot (>= 475 words).
+// rows0 for the pipelined kernel.  The raw-plane rows go through a ring of four registers (row r + 4 of this block
+// is requested when row r is done, then rows 0-3 of the next block `nx`); at row 4 the next round's stream chunks and
+// the next block's activations are requested.  `valid` is false for a half-wave without a block in the last round
+// (it decodes a copy of the tile's last block and stores nothing).
+template <int ELEM, int MODE, bool XBF16>
+__device__ __forceinline__ float rows0_ring(const LutLds &s, const uint32_t *words, const BlockArgs &a, const Shape &f,
+                                            const XRegs<XBF16> &x, uint4 ring[4], const Coord0 &c, const Coord0 &nx,
+                                            bool valid, Bulk &Bk, const Region &Rn, XRegs<XBF16> &xn, uint32_t tid,
+                                            uint32_t nth, uint32_t L) {
+    Seq<ELEM> S;
+    S.init(words);
+    float acc[8];
+#pragma unroll
+    for (int r = 0; r < (int)kRows0; r++) {
+        if (r == 4) {
+            bulk_issue(Bk, a.data, Rn, tid, nth);
+            if (MODE != kDequant) load_x16<XBF16>(xn, a.x, nx.col0, nx.col_ok);
+        }
+        uint32_t pw[8];
+        const float sum = row0<ELEM, MODE, XBF16>(S, s, ring[r & 3], x, pw);
+        ring[r & 3] = r < 4 ? raw_row0<ELEM>(a.low, f, c.row0 + r + 4, c.col0, c.col_ok)
+                            : raw_row0<ELEM>(a.low, f, nx.row0 + r - 4, nx.col0, nx.col_ok);
+        if (MODE == kDequant) store_row0<MODE>(a, f, valid ? c.row0 + r : f.M, c.col0, c.col_ok, pw);
+        else acc[r] = c.col_ok ? sum : 0.f;
+    }
+    return MODE == kDequant ? 0.f : reduce8_transposed(acc, L);
+}
+
+// The same for a block of a round whose streams do not fit the region buffer: decoded straight from global memory
+// with a rolled row loop and its own raw loads (compact code; such rounds are rare, e.g. near-uniform exponent
+// distributions).  Lanes past K16 have empty streams; the callers point them at the block's first word: decoding zero
+// bits walks at most 96 words (all escapes), less than one block of such a round.
 template <int ELEM, int MODE, bool XBF16>
 __device__ __forceinline__ float rows0_global(const LutLds &s, const uint32_t *words, const BlockArgs &a, const Shape &f,
-                                              const XRegs<XBF16> &x, const Coord0 &c, uint32_t L) {
-    Window<ELEM, const uint32_t *> W;
-    W.init(words);
+                                              const XRegs<XBF16> &x, const Coord0 &c, bool valid, uint32_t L) {
+    Seq<ELEM> S;
+    S.init(words);
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll 1
     for (int r = 0; r < (int)kRows0; r++) {
         const uint4 cur = raw_row0<ELEM>(a.low, f, c.row0 + r, c.col0, c.col_ok);
-        float sum = 0.f;
         uint32_t pw[8];
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-            uint32_t e1, e2;
-            W.quad(s, e1, e2);
-            use_quad<MODE, XBF16>(e1, e2, u4_get(cur, k), k, x, sum, pw);
-        }
+        const float sum = row0<ELEM, MODE, XBF16>(S, s, cur, x, pw);
         if (MODE == kDequant) {
-            store_row0<MODE>(a, f, c.row0 + r, c.col0, c.col_ok, pw);
+            store_row0<MODE>(a, f, valid ? c.row0 + r : f.M, c.col0, c.col_ok, pw);
         } else {
 #pragma unroll
             for (int i = 0; i < (int)kRows0 - 1; i++) acc[i] = acc[i + 1];    // rotation: at the end acc[i] = row i
@@ -158,183 +244,102 @@ __device__ __forceinline__ float rows0_global(const LutLds &s, const uint32_t *w
     return MODE == kDequant ? 0.f : reduce8_transposed(acc, L);
 }
 
-// Layout 0, one block per half-wave (tile of at most one block per half; also the fallback when LDS allows no
-// second slot).  Everything a block needs is requested before the table is staged.
-template <int ELEM, int MODE, bool XBF16>
+// Layout 0.  A workgroup owns G whole row groups (nt = G * CB blocks) and works through them in rounds of H blocks,
+// one per half-wave; a round's streams are staged once into a region buffer of slot_words * H words.
+//   PIPE = false (tiles of at most H blocks, small matrices; the launch plan guarantees it): every input is
+//     requested before the decode table is staged, then one copy of the tile's streams.
+//   PIPE = true: two region buffers; while round k decodes, round k + 1's streams, raw rows (four-register ring) and
+//     activations are in flight and round k + 2's bounds and header bytes are read, so after the first round no step
+//     waits on global memory.  One barrier per round publishes the next region.
+template <int ELEM, int MODE, bool XBF16, bool PIPE>
 __global__ void __launch_bounds__(1024) k_layout0(BlockArgs a) {
     __shared__ LutLds s;
     extern __shared__ uint32_t dyn[];
-    const uint32_t tid = threadIdx.x, L = tid & 31;
-    const uint32_t hw = tid >> 5, nhw = blockDim.x >> 5;
-    uint32_t *slot = dyn + hw * a.slot_words;
-    float *part = (float *)(dyn + nhw * a.slot_words);
+    const uint32_t tid = threadIdx.x, nth = blockDim.x, L = tid & 31;
+    const uint32_t hw = tid >> 5, H = nth >> 5;
+    const uint32_t cap = a.slot_words * H;                    // words per region buffer
+    uint32_t *cur = dyn, *nxt = dyn + cap;
+    float *part = (float *)(dyn + (PIPE ? 2u : 1u) * cap);
     const Shape f(a.M, a.K, 0);
     const uint32_t rg0 = blockIdx.x * a.G;
     const uint32_t ng = min(a.G, f.groups() - rg0);
-    const uint32_t nt = ng * f.CB;
+    const uint32_t nt = ng * f.CB, tl = nt - 1u;              // look-ahead past the tile re-reads block tl
+    const uint32_t B0 = rg0 * f.CB, nb = f.nb;
+    const uint32_t mend = B0 + nt == nb ? matrix_end(a, nb) : 0u;
+    // request order: region bounds and table first, then the stream copy (which needs the bounds), then the raw rows
+    // and activations; loads complete in order, so each wait below covers only what it needs
+    Region R = region_of(a, B0, B0 + min(H, nt), nb, mend);
+    LutLoad Q;
+    lut_issue(Q, a.lut);
     uint32_t t = hw;
-    Coord0 c = coord0(min(t, nt - 1), rg0, f, L);
+    Coord0 c = coord0(min(t, tl), rg0, f, L);
     uint32_t n = a.hdr[(uint64_t)c.b * kHdrBytes + L], base = a.bases[c.b];
-    uint4 raw[8];
-#pragma unroll
-    for (int r = 0; r < (int)kRows0; r++) raw[r] = raw_row0<ELEM>(a.low, f, c.row0 + r, c.col0, c.col_ok);
+    Bulk Bk;
+    bulk_issue(Bk, a.data, R, tid, nth);
     XRegs<XBF16> x;
     if (MODE != kDequant) load_x16<XBF16>(x, a.x, c.col0, c.col_ok);
-    stage_lut(s, a.lut);
-    while (t < nt) {
-        const uint32_t incl = half_scan_incl(n, L);
-        const uint32_t total = __shfl(incl, 31, 32), start = incl - n;
-        uint32_t sh;
-        float v;
-        if (stage_block(slot, a.slot_words, a.data, base, total, L, sh))
-            v = rows0<ELEM, MODE, XBF16>(s, slot + sh + start, a, f, x, raw, c, L);
-        else
-            v = rows0_global<ELEM, MODE, XBF16>(s, (const uint32_t *)(a.data + base) + (c.col_ok ? start : 0u), a, f, x, c, L);
-        if (MODE != kDequant && (L & 3) == 0) part[(c.g * kRows0 + (L >> 2)) * f.CB + c.cb] = v;
-        t += nhw;
-        if (t >= nt) break;
-        __builtin_amdgcn_wave_barrier();                        // the slot is overwritten by the next block
-        c = coord0(t, rg0, f, L);
-        n = a.hdr[(uint64_t)c.b * kHdrBytes + L];
-        base = a.bases[c.b];
+
+    if constexpr (!PIPE) {
+        // the table is stored before the raw rows are requested, so its registers are free for them
+        lut_commit<kLutSeq>(s, Q, a.lut);
+        uint4 raw[8];
 #pragma unroll
         for (int r = 0; r < (int)kRows0; r++) raw[r] = raw_row0<ELEM>(a.low, f, c.row0 + r, c.col0, c.col_ok);
-        if (MODE != kDequant) load_x16<XBF16>(x, a.x, c.col0, c.col_ok);
-    }
-    if (MODE != kDequant) finish_rows<MODE>(a, part, rg0 * kRows0, ng * kRows0, f.CB);
-}
-
-// A block's stream words copied ahead: four 16-byte loads per lane cover a 512-word slot (lanes past the block
-// re-read its last chunk, so the count is fixed), written to LDS once the slot is free.
-struct Ahead {
-    u32x4_t v0, v1, v2, v3;     // native vectors: HIP's uint4 struct copies would go through a stack object
-    uint32_t need, sh;
-    bool fits;
-};
-__device__ __forceinline__ void ahead_issue(Ahead &A, const uint8_t *__restrict__ data, uint32_t base, uint32_t total,
-                                            uint32_t L, uint32_t slot_words) {
-    const uint8_t *p = data + (base & ~15u);
-    A.sh = (base & 15u) >> 2;
-    A.need = A.sh + total + 3;
-    A.fits = A.need <= slot_words;
-    const uint32_t last = (min(A.need, slot_words) - 1u) & ~3u;
-    A.v0 = *(const u32x4_t *)(p + 4u * min(L * 4u, last));
-    A.v1 = *(const u32x4_t *)(p + 4u * min(L * 4u + 128u, last));
-    A.v2 = *(const u32x4_t *)(p + 4u * min(L * 4u + 256u, last));
-    A.v3 = *(const u32x4_t *)(p + 4u * min(L * 4u + 384u, last));
-}
-__device__ __forceinline__ void ahead_commit(const Ahead &A, uint32_t *slot, uint32_t L) {
-    if (!A.fits) return;
-    const uint32_t i = L * 4u;
-    if (i < A.need) *(u32x4_t *)(slot + i) = A.v0;
-    if (i + 128u < A.need) *(u32x4_t *)(slot + i + 128u) = A.v1;
-    if (i + 256u < A.need) *(u32x4_t *)(slot + i + 256u) = A.v2;
-    if (i + 384u < A.need) *(u32x4_t *)(slot + i + 384u) = A.v3;
-}
-
-// Inputs of the next block, requested half a block ahead of their use.
-template <bool XBF16>
-struct Next0 {
-    Ahead A;                    // stream words for its LDS slot
-    XRegs<XBF16> x;             // activations
-    uint32_t start;             // lane's first word inside the block
-};
-
-template <int ELEM, int MODE, bool XBF16>
-__device__ __forceinline__ void next_issue(Next0<XBF16> &N, const BlockArgs &a, const Coord0 &nx, uint32_t n_n, uint32_t base_n,
-                                           uint32_t L) {
-    const uint32_t incl = half_scan_incl(n_n, L);
-    N.start = incl - n_n;
-    ahead_issue(N.A, a.data, base_n, __shfl(incl, 31, 32), L, a.slot_words);
-    if (MODE != kDequant) load_x16<XBF16>(N.x, a.x, nx.col0, nx.col_ok);
-}
-
-// rows0 for the pipelined kernel: the raw-plane rows go through a ring of four registers (row r + 4 of this block is
-// requested when row r is done, then rows 0-3 of the next block), and the next block's stream words and activations
-// are requested at row 4.  Register cost of the look-ahead: 16 (ring) + 16 (stream) + activations.
-template <int ELEM, int MODE, bool XBF16>
-__device__ __forceinline__ float rows0_ring(const LutLds &s, const uint32_t *words, const BlockArgs &a, const Shape &f,
-                                            const XRegs<XBF16> &x, uint4 ring[4], const Coord0 &c, const Coord0 &nx,
-                                            uint32_t n_n, uint32_t base_n, Next0<XBF16> &N, uint32_t L) {
-    Window<ELEM, const uint32_t *> W;
-    W.init(words);
-    float acc[8];
-#pragma unroll
-    for (int r = 0; r < (int)kRows0; r++) {
-        if (r == 4) next_issue<ELEM, MODE, XBF16>(N, a, nx, n_n, base_n, L);
-        float sum = 0.f;
-        uint32_t pw[8];
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-            uint32_t e1, e2;
-            W.quad(s, e1, e2);
-            use_quad<MODE, XBF16>(e1, e2, u4_get(ring[r & 3], k), k, x, sum, pw);
-            if (MODE == kDequant) asm volatile("" : "+v"(pw[2 * k]), "+v"(pw[2 * k + 1]));
-            else asm volatile("" : "+v"(sum));
-        }
-        ring[r & 3] = r < 4 ? raw_row0<ELEM>(a.low, f, c.row0 + r + 4, c.col0, c.col_ok)
-                            : raw_row0<ELEM>(a.low, f, nx.row0 + r - 4, nx.col0, nx.col_ok);
-        if (MODE == kDequant) store_row0<MODE>(a, f, c.row0 + r, c.col0, c.col_ok, pw);
-        else acc[r] = c.col_ok ? sum : 0.f;
-    }
-    return MODE == kDequant ? 0.f : reduce8_transposed(acc, L);
-}
-
-// Layout 0, several blocks per half-wave, software-pipelined over two LDS slots per half: while block t decodes from
-// one slot, the stream words, raw rows and activations of block t + H (H = half-waves of the workgroup) are in flight
-// and the header and base of block t + 2H are read, so after the first block no step waits on global memory.
-template <int ELEM, int MODE, bool XBF16>
-__global__ void __launch_bounds__(1024) k_layout0_pipe(BlockArgs a) {
-    __shared__ LutLds s;
-    extern __shared__ uint32_t dyn[];
-    const uint32_t tid = threadIdx.x, L = tid & 31;
-    const uint32_t hw = tid >> 5, nhw = blockDim.x >> 5;
-    uint32_t *cur = dyn + hw * 2u * a.slot_words, *nxt = cur + a.slot_words;
-    float *part = (float *)(dyn + nhw * 2u * a.slot_words);
-    const Shape f(a.M, a.K, 0);
-    const uint32_t rg0 = blockIdx.x * a.G;
-    const uint32_t ng = min(a.G, f.groups() - rg0);
-    const uint32_t nt = ng * f.CB, tl = nt - 1;               // look-ahead past the tile re-reads block tl
-    uint32_t t = hw;
-    Coord0 c = coord0(min(t, tl), rg0, f, L), cn = coord0(min(t + nhw, tl), rg0, f, L);
-    const uint32_t n = a.hdr[(uint64_t)c.b * kHdrBytes + L], base = a.bases[c.b];
-    uint32_t n_n = a.hdr[(uint64_t)cn.b * kHdrBytes + L], base_n = a.bases[cn.b];
-    uint4 ring[4];
-#pragma unroll
-    for (int r = 0; r < 4; r++) ring[r] = raw_row0<ELEM>(a.low, f, c.row0 + r, c.col0, c.col_ok);
-    XRegs<XBF16> x;
-    if (MODE != kDequant) load_x16<XBF16>(x, a.x, c.col0, c.col_ok);
-    stage_lut(s, a.lut);
-    if (t < nt) {
-        const uint32_t incl = half_scan_incl(n, L);
-        uint32_t start = incl - n, sh;
-        bool fits = stage_block(cur, a.slot_words, a.data, base, __shfl(incl, 31, 32), L, sh);
-        uint32_t base_c = base;
-        for (;;) {
-            const Coord0 cnn = coord0(min(t + 2u * nhw, tl), rg0, f, L);
-            const uint32_t n_nn = a.hdr[(uint64_t)cnn.b * kHdrBytes + L], base_nn = a.bases[cnn.b];
-            Next0<XBF16> N;
+        const bool fits = R.n16 * 4u <= cap;
+        if (fits) bulk_commit(Bk, cur, R, tid, nth);
+        __syncthreads();
+        if (t < nt) {
+            const uint32_t start = c.col_ok ? half_scan_incl(n, L) - n : 0u;
             float v;
-            if (fits) {
-                v = rows0_ring<ELEM, MODE, XBF16>(s, cur + sh + start, a, f, x, ring, c, cn, n_n, base_n, N, L);
+            if (fits) v = rows0<ELEM, MODE, XBF16>(s, cur + ((base - R.lo16) >> 2) + start, a, f, x, raw, c, L);
+            else v = rows0_global<ELEM, MODE, XBF16>(s, (const uint32_t *)(a.data + base) + start, a, f, x, c, true, L);
+            if (MODE != kDequant && (L & 3) == 0) part[(c.g * kRows0 + (L >> 2)) * f.CB + c.cb] = v;
+        }
+    } else {
+        uint4 ring[4];
+#pragma unroll
+        for (int r = 0; r < 4; r++) ring[r] = raw_row0<ELEM>(a.low, f, c.row0 + r, c.col0, c.col_ok);
+        Coord0 cn = coord0(min(t + H, tl), rg0, f, L);
+        uint32_t n_n = a.hdr[(uint64_t)cn.b * kHdrBytes + L], base_n = a.bases[cn.b];
+        Region Rn = region_of(a, B0 + min(H, tl), B0 + min(2u * H, nt), nb, mend);
+        lut_commit<kLutSeq>(s, Q, a.lut);
+        if (R.n16 * 4u <= cap) bulk_commit(Bk, cur, R, tid, nth);
+        __syncthreads();
+        const uint32_t rounds = (nt + H - 1u) / H;
+        uint32_t start = c.col_ok ? half_scan_incl(n, L) - n : 0u;
+        for (uint32_t k = 0;; k++) {
+            // round k + 2: this half-wave's header byte and base, and the region bounds
+            const Coord0 cnn = coord0(min(t + 2u * H, tl), rg0, f, L);
+            const uint32_t n_nn = a.hdr[(uint64_t)cnn.b * kHdrBytes + L], base_nn = a.bases[cnn.b];
+            const Region Rnn = region_of(a, B0 + min((k + 2u) * H, tl), B0 + min((k + 3u) * H, nt), nb, mend);
+            const bool valid = t < nt;
+            XRegs<XBF16> xn;
+            float v;
+            if (R.n16 * 4u <= cap) {
+                v = rows0_ring<ELEM, MODE, XBF16>(s, cur + ((base - R.lo16) >> 2) + start, a, f, x, ring, c, cn, valid, Bk,
+                                                  Rn, xn, tid, nth, L);
             } else {
-                next_issue<ELEM, MODE, XBF16>(N, a, cn, n_n, base_n, L);
-                v = rows0_global<ELEM, MODE, XBF16>(s, (const uint32_t *)(a.data + base_c) + (c.col_ok ? start : 0u), a, f, x, c, L);
+                bulk_issue(Bk, a.data, Rn, tid, nth);
+                if (MODE != kDequant) load_x16<XBF16>(xn, a.x, cn.col0, cn.col_ok);
+                v = rows0_global<ELEM, MODE, XBF16>(s, (const uint32_t *)(a.data + base) + start, a, f, x, c, valid, L);
 #pragma unroll
                 for (int r = 0; r < 4; r++) ring[r] = raw_row0<ELEM>(a.low, f, cn.row0 + r, cn.col0, cn.col_ok);
             }
-            if (MODE != kDequant && (L & 3) == 0) part[(c.g * kRows0 + (L >> 2)) * f.CB + c.cb] = v;
-            t += nhw;
-            if (t >= nt) break;
-            ahead_commit(N.A, nxt, L);
-            __builtin_amdgcn_wave_barrier();
+            if (valid && MODE != kDequant && (L & 3) == 0) part[(c.g * kRows0 + (L >> 2)) * f.CB + c.cb] = v;
+            if (k + 1u >= rounds) break;
+            if (Rn.n16 * 4u <= cap) bulk_commit(Bk, nxt, Rn, tid, nth);
+            __syncthreads();                                     // region k + 1 visible; region k free
             uint32_t *tmp = cur; cur = nxt; nxt = tmp;
-            start = N.start; sh = N.A.sh; fits = N.A.fits; base_c = base_n;
-            if (MODE != kDequant) x = N.x;
+            start = cn.col_ok ? half_scan_incl(n_n, L) - n_n : 0u;
+            base = base_n;
+            R = Rn;
+            Rn = Rnn;
+            if (MODE != kDequant) x = xn;
             c = cn;
             cn = cnn;
             n_n = n_nn;
             base_n = base_nn;
+            t += H;
         }
     }
     if (MODE != kDequant) finish_rows<MODE>(a, part, rg0 * kRows0, ng * kRows0, f.CB);
@@ -406,7 +411,7 @@ template <int ELEM, int MODE, bool XBF16>
 __global__ void __launch_bounds__(1024) k_layout1(BlockArgs a) {
     __shared__ LutLds s;
     extern __shared__ uint32_t dyn[];
-    stage_lut(s, a.lut);
+    stage_lut<kLutWindow>(s, a.lut);
     constexpr uint32_t RB = ELEM == kElemFp8 ? 8u : 16u;           // raw bytes per lane and super-chunk
     const uint32_t tid = threadIdx.x, L = tid & 31, r = L >> 2, q = L & 3;
     const uint32_t hw = tid >> 5, nhw = blockDim.x >> 5;
@@ -470,7 +475,7 @@ template <int ELEM>
 __global__ void __launch_bounds__(256) k_gather0(GatherArgs a) {
     __shared__ LutLds s;
     extern __shared__ uint32_t dyn[];
-    stage_lut(s, a.lut);
+    stage_lut<kLutWindow>(s, a.lut);
     const uint32_t L = threadIdx.x & 31, hw = threadIdx.x >> 5;
     uint32_t *slot = dyn + hw * a.slot_words;
     const uint32_t id = blockIdx.x * (blockDim.x >> 5) + hw;
@@ -520,7 +525,7 @@ template <int ELEM>
 __global__ void __launch_bounds__(256) k_gather1(GatherArgs a) {
     __shared__ LutLds s;
     extern __shared__ uint32_t dyn[];
-    stage_lut(s, a.lut);
+    stage_lut<kLutWindow>(s, a.lut);
     constexpr uint32_t RB = ELEM == kElemFp8 ? 8u : 16u;
     const uint32_t L = threadIdx.x & 31, r = L >> 2, q = L & 3, hw = threadIdx.x >> 5;
     uint32_t *slot = dyn + hw * a.slot_words;
@@ -551,9 +556,9 @@ __global__ void __launch_bounds__(256) k_gather1(GatherArgs a) {
 template <int ELEM, int MODE, bool XBF16>
 static int launch_prefix_t(const LaunchPlan &p, const BlockArgs &a, hipStream_t st) {
     if (p.layout == 0 && p.pipe)
-        hipLaunchKernelGGL((k_layout0_pipe<ELEM, MODE, XBF16>), dim3(p.grid), dim3(p.threads), p.lds, st, a);
+        hipLaunchKernelGGL((k_layout0<ELEM, MODE, XBF16, true>), dim3(p.grid), dim3(p.threads), p.lds, st, a);
     else if (p.layout == 0)
-        hipLaunchKernelGGL((k_layout0<ELEM, MODE, XBF16>), dim3(p.grid), dim3(p.threads), p.lds, st, a);
+        hipLaunchKernelGGL((k_layout0<ELEM, MODE, XBF16, false>), dim3(p.grid), dim3(p.threads), p.lds, st, a);
     else
         hipLaunchKernelGGL((k_layout1<ELEM, MODE, XBF16>), dim3(p.grid), dim3(p.threads), p.lds, st, a);
     return (int)hipGetLastError();

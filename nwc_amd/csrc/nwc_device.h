@@ -86,33 +86,69 @@ __device__ __forceinline__ float reduce8_transposed(float acc[8], uint32_t L) {
 }
 
 // ---- decode table in LDS ----
-// The stored 4096-word LUT is re-encoded once per workgroup:
-//   two complete codes:  byte 0 = 32 - c (c = bits of both codes, 4..12), bytes 1/2 = exponent bytes, byte 3 = 0
-//   anything else:       bit 31 set (slow path)
-// Byte 0 is then directly the v_alignbit shift that advances the window by c, and two entries added give the
-// shift for both pairs in their low 5 bits and 64 - c1 - c2 in byte 0.
+// The stored 4096-word LUT is re-encoded once per workgroup.  Entries that are not two complete codes get bit 31 (slow
+// path); for the others byte 0 (c = bits of both codes, 4..12) becomes
+//   kLutWindow: 32 - c, the funnel shift that advances a register window by c (Window);
+//   kLutSeq:    18 - c, the right shift that puts the second code pair's 12 bits at [13:2] (Seq); two entries added
+//               give 36 - (c1 + c2) in byte 0.
+// Bytes 1/2 keep the two exponent bytes.
+enum LutKind { kLutWindow = 0, kLutSeq = 1 };
+
 struct LutLds {
     uint32_t tab[kLutWords];
     uint8_t eor[16];            // exp_of_rank, read back from the table (the slow path's rank -> byte map)
 };
 
-__device__ __forceinline__ void stage_lut(LutLds &s, const uint32_t *__restrict__ lut) {
+template <int KIND>
+__device__ __forceinline__ uint32_t lut_transform(uint32_t e) {
+    if (e & kFlag) return e | 0x80000000u;
+    const uint32_t c = e & 0xFFu;
+    return (e & 0xFFFFFF00u) | (KIND == kLutWindow ? ((32u - c) & 31u) : (18u - c));
+}
+
+// Table staging split in two so its loads overlap other requests: lut_issue reads the first 4 * blockDim 16-byte
+// chunks (all 1024 for >= 256 threads) and the word exp_of_rank[tid & 15] comes from; lut_commit re-encodes and
+// stores them (and any remaining chunks).  The caller publishes the table with a barrier.
+struct LutLoad {
+    u32x4_t v0, v1, v2, v3;
+    uint32_t ew;
+};
+__device__ __forceinline__ void lut_issue(LutLoad &Q, const uint32_t *__restrict__ lut) {
     const uint32_t tid = threadIdx.x, nth = blockDim.x;
-    for (uint32_t i = tid; i < kLutWords / 4; i += nth) {
-        uint4 v = ((const uint4 *)lut)[i];
-        uint32_t e[4] = {v.x, v.y, v.z, v.w};
+    constexpr uint32_t n4 = kLutWords / 4;
+    // source word of exp_of_rank[q]: pattern "q zeros, one, sign 0" for q < 11; ranks 11-14 sit in bytes 1/2 of
+    // entries 0 and 1 (11, 13: byte 1; 12, 14: byte 2); slot 15 is unused
+    const uint32_t q = tid & 15u;
+    Q.ew = lut[q < 11u ? (1u << (kPeek - 1u - q)) : q < 15u ? (q - 11u) >> 1 : 0u];
+    const u32x4_t *l4 = (const u32x4_t *)lut;
+    Q.v0 = l4[min(tid, n4 - 1u)];
+    Q.v1 = l4[min(tid + nth, n4 - 1u)];
+    Q.v2 = l4[min(tid + 2u * nth, n4 - 1u)];
+    Q.v3 = l4[min(tid + 3u * nth, n4 - 1u)];
+}
+template <int KIND>
+__device__ __forceinline__ void lut_store4(LutLds &s, uint32_t i, u32x4_t e) {
 #pragma unroll
-        for (int k = 0; k < 4; k++)
-            e[k] = (e[k] & kFlag) ? (e[k] | 0x80000000u) : ((e[k] & 0xFFFFFF00u) | ((32u - (e[k] & 0xFFu)) & 31u));
-        ((uint4 *)s.tab)[i] = make_uint4(e[0], e[1], e[2], e[3]);
-    }
-    if (tid < 16) {
-        uint32_t e, sh = 8;
-        if (tid < 11) e = lut[1u << (kPeek - 1 - tid)];          // pattern "r zeros, one, sign 0"
-        else if (tid < 15) { e = lut[(tid - 11) >> 1]; sh = (tid & 1) ? 8 : 16; }   // 11,13: byte 1; 12,14: byte 2
-        else e = 0;
-        s.eor[tid] = (uint8_t)((e >> sh) & 0x7Fu);
-    }
+    for (int j = 0; j < 4; j++) e[j] = lut_transform<KIND>(e[j]);
+    ((u32x4_t *)s.tab)[i] = e;
+}
+template <int KIND>
+__device__ __forceinline__ void lut_commit(LutLds &s, const LutLoad &Q, const uint32_t *__restrict__ lut) {
+    const uint32_t tid = threadIdx.x, nth = blockDim.x;
+    constexpr uint32_t n4 = kLutWords / 4;
+    if (tid < n4) lut_store4<KIND>(s, tid, Q.v0);
+    if (tid + nth < n4) lut_store4<KIND>(s, tid + nth, Q.v1);
+    if (tid + 2u * nth < n4) lut_store4<KIND>(s, tid + 2u * nth, Q.v2);
+    if (tid + 3u * nth < n4) lut_store4<KIND>(s, tid + 3u * nth, Q.v3);
+    for (uint32_t i = tid + 4u * nth; i < n4; i += nth) lut_store4<KIND>(s, i, ((const u32x4_t *)lut)[i]);   // < 256 threads
+    const uint32_t q = tid & 15u;
+    if (tid < 16) s.eor[tid] = q == 15u ? 0 : (uint8_t)((Q.ew >> ((q < 11u || (q & 1u)) ? 8u : 16u)) & 0x7Fu);
+}
+template <int KIND>
+__device__ __forceinline__ void stage_lut(LutLds &s, const uint32_t *__restrict__ lut) {
+    LutLoad Q;
+    lut_issue(Q, lut);
+    lut_commit<KIND>(s, Q, lut);
     __syncthreads();
 }
 
@@ -197,6 +233,73 @@ struct Window {
 
     // skip four codes (gather: rows in front of the wanted one)
     __device__ __forceinline__ void skip_quad(const LutLds &s) { uint32_t a, b; quad(s, a, b); }
+};
+
+// ---- bit cursor over an LDS-staged lane stream ----
+// P = bit position of the next code (0 = the MSB of the lane's word 0).  The cursor keeps nm = ~(P - 1), the word
+// pointer wp = lane + ((P - 1) >> 5) and the words A = wp[0], B = wp[1], C = wp[2]; the 32 bits from P are then
+// alignbit(A, B, nm) (the shift takes nm's low five bits, 31 - ((P - 1) & 31)).  An advance by c <= 24 bits moves
+// at most one word, exactly when c > (nm & 31): A, B <- B, C, and the new C is read for the step after next.  So no
+// read of stream words lies on the dependency chain of a step, which is
+//   window -> table read (kLutSeq encoding) -> shift -> table read -> add -> compare -> select -> window.
+// The words may live in LDS (staged streams) or global memory (fallback).
+template <int ELEM>
+struct Seq {
+    const uint32_t *wp;
+    int32_t nm;
+    uint32_t A, B, C;
+
+    // At P = 0, P - 1 = -1 lies in word -1, whose value is never used: shift 0 selects B, and the first step always
+    // moves a word.  It is not read either (word -1 of a global stream may precede the allocation).
+    __device__ __forceinline__ void init(const uint32_t *lane) {
+        wp = lane - 1;
+        nm = 0;
+        A = 0u; B = lane[0]; C = lane[1];
+    }
+    __device__ __forceinline__ uint32_t window() const { return __builtin_amdgcn_alignbit(A, B, (uint32_t)nm); }
+    __device__ __forceinline__ void step(bool crossed, int32_t nm2) {
+        nm = nm2;
+        A = crossed ? B : A;
+        B = crossed ? C : B;
+        wp = crossed ? wp + 1 : wp;
+        C = wp[2];
+    }
+    // re-read the cached words after the position was reset (at P = 0 word -1 is replaced by word 0, see init)
+    __device__ __forceinline__ void reload() { A = wp[nm == 0 ? 1 : 0]; B = wp[1]; C = wp[2]; }
+
+    // Four codes = two pairs from two table reads; e1 holds the exponent bytes of weights 0,1 in bytes 1,2 and e2
+    // those of weights 2,3.  Correct only if neither entry has bit 31; otherwise the caller resets the position and
+    // redoes the step with slow_quad.
+    __device__ __forceinline__ void fast_quad(const LutLds &s, uint32_t &e1, uint32_t &e2) {
+        const uint32_t hi = window();
+        e1 = lds_entry(s, (hi >> 18) & 0x3FFCu);
+        e2 = lds_entry(s, (hi >> (e1 & 31u)) & 0x3FFCu);               // the 12 bits after the first c1
+        const uint32_t db = (e1 + e2) & 0xFFu;                         // 36 - c, c = c1 + c2 (kLutSeq table)
+        step(db < 36u - ((uint32_t)nm & 31u), nm - 36 + (int32_t)db);
+    }
+
+    // one code by counting leading zeros: rank r < max -> r zeros, one, sign; BF16 escape -> 15 zeros, one, byte
+    __device__ __forceinline__ uint32_t slow_code(const LutLds &s) {
+        const uint32_t hi = window();
+        uint32_t u = __clz((int)hi), b, c;
+        if (ELEM == kElemFp8 || u < kMaxRankBf16) {
+            u = u < 15u ? u : 15u;
+            b = (((hi >> (30u - u)) & 1u) << 7) | s.eor[u];
+            c = u + 2u;
+        } else {
+            b = (hi >> 8) & 0xFFu;
+            c = 24u;
+        }
+        step(c > ((uint32_t)nm & 31u), nm - (int32_t)c);
+        return b;
+    }
+    __device__ __forceinline__ void slow_quad(const LutLds &s, uint32_t &e1, uint32_t &e2) {
+        uint32_t bytes = 0;                                            // b3 b2 b1 b0 after four codes
+#pragma unroll 1
+        for (int k = 0; k < 4; k++) bytes = (bytes >> 8) | (slow_code(s) << 24);
+        e1 = (bytes << 8) & 0x00FFFF00u;
+        e2 = (bytes >> 8) & 0x00FFFF00u;
+    }
 };
 
 // Per-block lane offsets: n = words of lane L, start = words of the lanes before it, total = words of the block.
