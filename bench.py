@@ -9,9 +9,11 @@ and replayed.  Weights are N(0, 0.02^2) from fixed seeds; each of the four matri
 36 distinct device buffers (the sweep reads 36 x 4 different buffers, far beyond the 256 MB Infinity Cache).
 
 Reported: value = algorithmic bytes per token / GPU time per token (GB/s), with the per-launch medians (HIP events),
-the same sweep with hipBLASLt BF16 matvecs (F.linear), the roofline of the dominant kernel and the CPU baseline (the
-C oracle's decode + fp32 matvec of configs[0], on the host cores).
+the same sweep with hipBLASLt BF16 matvecs (F.linear), the roofline of the dominant kernel (the gate_up launch:
+algorithmic bytes / average launch time; HBM traffic from the committed counter summary profiles/traffic_gate_up.json)
+and the CPU baseline (the C oracle's decode + fp32 matvec of configs[0], on the host cores).
 usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--layout 0] [--cpu-seconds 10]
+       python bench.py --profile-launches 20     (counter target for rocprofv3 --pmc: copies + gate_up launches)
 """
 import argparse
 import ctypes
@@ -76,6 +78,32 @@ def event_ms(fn, runs, rotate):
         ev[i][1].record()
     torch.cuda.synchronize()
     return statistics.median(a.elapsed_time(b) for a, b in ev), [a.elapsed_time(b) for a, b in ev]
+
+
+def avg_launch_ms(fn, rotate, replays):
+    """Average GPU time per launch: `rotate` back-to-back launches captured as one HIP graph, replayed `replays` times
+    between two HIP events on the launch stream (a graph leaves no launch gaps, so this is the kernel's own time)."""
+    import torch
+    for i in range(rotate):
+        fn(i)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(rotate):
+            fn(i)
+    g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(replays):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / (rotate * replays)
+
+
+DOMINANT = "gate_up"            # the roofline's kernel: the largest matrix, k_layout0<BF16, token, BF16 x, pipelined>
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_gate_up.json")
 
 
 def run_gpu(args):
@@ -197,11 +225,16 @@ def run_gpu(args):
         del wcopy
         torch.cuda.empty_cache()
 
+    # ---- roofline of the dominant kernel: average launch time of back-to-back gate_up launches ----
+    name, M, K, c, x, w = next(b for b in base if b[0] == DOMINANT)
+    L = launches[name]
+    dom_bytes = c.bytes + 2 * K + 2 * M
+    dom_ms = avg_launch_ms(lambda j: L[j](ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)), LAYERS, 4)
     sum_launch_us = LAYERS * sum(p["nwc_us"] for p in per)
-    achieved = bytes_tok / (sum_launch_us * 1e-6) / 1e9
     return {
         "ms_step": ms_step, "graph": graph is not None, "bytes_tok": bytes_tok, "bf16_tok": bf16_tok, "per": per,
-        "sum_launch_us": sum_launch_us, "achieved": achieved, "blas": blas,
+        "sum_launch_us": sum_launch_us, "dom_bytes": dom_bytes, "dom_us": dom_ms * 1e3,
+        "achieved": dom_bytes / (dom_ms * 1e-3) / 1e9, "blas": blas,
         "device": {"name": props.name, "arch": props.gcnArchName, "cus": props.multi_processor_count},
     }
 
@@ -234,6 +267,42 @@ def run_cpu(args):
             "us_per_matvec": round(dt / reps * 1e6, 1)}
 
 
+def traffic_bytes():
+    """HBM bytes per gate_up launch from the committed rocprofv3 counter summary (FETCH_SIZE + WRITE_SIZE, each scaled
+    by the factor a plain copy of known size gives), or None when there is none."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            return json.load(f)["bytes_per_launch"]
+    except (OSError, ValueError, KeyError):
+        return None
+
+
+def run_profile(args):
+    """Counter target: --profile-launches gate_up launches, after three device copies of 256 MiB (the calibration
+    kernel of known size).  Run under rocprofv3 --pmc; prints one line per phase."""
+    import torch
+    from nwc_amd.nwc_torch import NWCWeight
+    dev = torch.device("cuda:0")
+    src = torch.empty(256 << 20, dtype=torch.uint8, device=dev).fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print("calibration: 3 copies of 268435456 bytes", flush=True)
+    del src, dst
+    name, M, K = next(s for s in SHAPES if s[0] == DOMINANT)
+    c = NWCWeight(make_weight(M, K, 1000 + [s[0] for s in SHAPES].index(DOMINANT)), device=dev, layout=args.layout)
+    cs = [c] + [clone_weight(c) for _ in range(7)]
+    x = torch.randn(K, generator=torch.Generator().manual_seed(2)).to(torch.bfloat16).to(dev)
+    ys = [torch.empty(M, dtype=torch.bfloat16, device=dev) for _ in cs]
+    L = [Launch(cc, x, y) for cc, y in zip(cs, ys)]
+    sh = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    for i in range(args.profile_launches):
+        L[i % len(L)](sh)
+    torch.cuda.synchronize()
+    print(f"{DOMINANT}: {args.profile_launches} launches, {c.bytes + 2 * K + 2 * M} algorithmic bytes each", flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -244,12 +313,17 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-baseline", action="store_true")
+    ap.add_argument("--profile-launches", type=int, default=0,
+                    help="only run the counter target (copies + this many gate_up launches), for rocprofv3 --pmc")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print("bench.py measures one GPU: this path (a batch-1 decode-matvec) is not run across GPUs in this build; "
               "use --gpus 1", file=sys.stderr)
         sys.exit(2)
+    if args.profile_launches:
+        run_profile(args)
+        return
 
     g = run_gpu(args)
     cpu = None if args.no_cpu else run_cpu(args)
@@ -274,9 +348,13 @@ def main():
         "hipblaslt": None if blas is None else {k: (round(v, 2) if isinstance(v, float) else v) for k, v in blas.items()},
         "speedup_vs_hipblaslt": None if blas is None else round(blas["us_per_token_graph"] / us_tok, 3),
         "roofline": {"bound": "hbm", "achieved": round(g["achieved"], 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": round(g["achieved"] / PEAK_HBM_GBS, 4), "traffic": None,
-                     "kernel": "k_layout0<BF16, token, bf16 x> (all four shapes)",
-                     "achieved_basis": "sum over the 4 shapes of (NWCWeight.bytes + x + y) / sum of per-launch median times"},
+                     "frac": round(g["achieved"] / PEAK_HBM_GBS, 4), "traffic": traffic_bytes(),
+                     "kernel": "k_layout0<0, 0, true, true> (BF16, token, BF16 x, pipelined): gate_up 19456x2560",
+                     "bytes_per_launch": g["dom_bytes"], "avg_launch_us": round(g["dom_us"], 2),
+                     "achieved_basis": "NWCWeight.bytes + x + y of one gate_up launch / average time of "
+                                       f"{4 * LAYERS} launches (a HIP graph of {LAYERS} back-to-back launches replayed 4 "
+                                       "times between HIP events on the launch stream)",
+                     "sweep_achieved": round(g["bytes_tok"] / (g["sum_launch_us"] * 1e-6) / 1e9, 1)},
         "cpu_baseline": cpu,
         "device": g["device"],
     }

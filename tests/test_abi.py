@@ -1,0 +1,82 @@
+"""The C-ABI library (nwc_amd/lib/nwc_ops.so) loads and exports every symbol include/nwc_ops.h declares, and its
+host entry points answer as the reference's do (nwc_ops.cu:100-126).  No device entry point is called here (CPU
+suite); the GPU tests call them through the same ABI."""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "nwc_ops.h")
+REFERENCE_EXPORTS = {"nwc_info", "nwc_layout", "nwc_encode", "nwc_build_tab", "nwc_matvec", "nwc_dequant",
+                     "nwc_linear_bf16", "nwc_gather", "nwc_ref_fp8", "nwc_setup"}      # nwc_ops.cu:27-39
+
+
+def _declared():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return set(re.findall(r"^\s*(?:int|int64_t|void)\s+(nwc_\w+)\s*\(", text, flags=re.M))
+
+
+def _lib():
+    from nwc_amd.nwc_torch import _LIB_PATH
+    return ctypes.CDLL(_LIB_PATH)
+
+
+def test_header_declares_the_reference_exports():
+    d = _declared()
+    assert REFERENCE_EXPORTS <= d
+    assert d - REFERENCE_EXPORTS == {"nwc_linear_xbf16"}
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib()
+    for name in sorted(_declared()):
+        assert hasattr(lib, name), f"{name} missing from the library"
+
+
+def test_info():
+    lib = _lib()
+    lib.nwc_info.restype = ctypes.c_int
+    lib.nwc_info.argtypes = [ctypes.c_int]
+    assert [lib.nwc_info(i) for i in range(8)] == [11, 1, 4096, 32, 4096, 1, 1, 1]
+    assert lib.nwc_info(8) == -1 and lib.nwc_info(-1) == -1
+
+
+@pytest.mark.parametrize("M,K,elem,expect", [
+    (19456, 2560, 0x00, (12160, 19456 * 2560, 19456 * 5, 2560)),      # nb, raw bytes, scratch, K16
+    (2560, 9728, 0x00, (6080, 2560 * 9728, 2560 * 19, 9728)),
+    (13, 40, 0x00, (2, 13 * 48, 16, 48)),                              # M * K16 raw bytes, Mp * CB
+])
+def test_layout_values(M, K, elem, expect):
+    lib = _lib()
+    lib.nwc_layout.restype = ctypes.c_int
+    lib.nwc_layout.argtypes = [ctypes.c_uint64, ctypes.c_uint32, ctypes.c_int, ctypes.c_void_p]
+    out = np.zeros(4, np.uint64)
+    assert lib.nwc_layout(M, K, elem, out.ctypes.data) == 0
+    assert tuple(int(v) for v in out) == expect
+
+
+def test_layout_matches_oracle():
+    from oracle import oracle as O
+    lib = _lib()
+    lib.nwc_layout.restype = ctypes.c_int
+    lib.nwc_layout.argtypes = [ctypes.c_uint64, ctypes.c_uint32, ctypes.c_int, ctypes.c_void_p]
+    out = np.zeros(4, np.uint64)
+    for M, K in [(1, 1), (7, 513), (19456, 2560), (4608, 3584), (152064, 3584)]:
+        for elem in (0, 1):
+            for layout in (0, 1, 2):
+                assert lib.nwc_layout(M, K, elem | layout << 4, out.ctypes.data) == 0
+                assert tuple(int(v) for v in out) == tuple(O.layout_info(M, K, elem, layout))
+
+
+def test_layout_rejects():
+    lib = _lib()
+    lib.nwc_layout.restype = ctypes.c_int
+    lib.nwc_layout.argtypes = [ctypes.c_uint64, ctypes.c_uint32, ctypes.c_int, ctypes.c_void_p]
+    out = np.zeros(4, np.uint64)
+    assert lib.nwc_layout(0, 16, 0, out.ctypes.data) == -1
+    assert lib.nwc_layout(16, 0, 0, out.ctypes.data) == -1
+    assert lib.nwc_layout(1 << 32, 16, 0, out.ctypes.data) == -1
