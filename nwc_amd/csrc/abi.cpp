@@ -24,9 +24,12 @@ int current_cus() {
 }
 
 // nwc_ops.cu:1050: the fixed block of 4096 weights, M = n / K within 32 bits, and a known element type / layout
+// This build also addresses the layout-0 raw plane with 32-bit offsets: M * K16 < 2^32 (4 GB planes).
 bool shape_ok(uint64_t n, uint32_t block, uint32_t K, int elem) {
-    return block == kBlock && K != 0 && n % K == 0 && n / K >= 1 && n / K <= 0xFFFFFFFFull && elem_type(elem) <= 1 &&
-           elem_layout(elem) <= 2 && (elem & ~0xFF) == 0;
+    if (!(block == kBlock && K != 0 && n % K == 0 && n / K >= 1 && n / K <= 0xFFFFFFFFull && elem_type(elem) <= 1 &&
+          elem_layout(elem) <= 2 && (elem & ~0xFF) == 0))
+        return false;
+    return (n / K) * (uint64_t)((K + 15u) & ~15u) < (1ull << 32);
 }
 
 // LDS words per half-wave for a staged block: an 8 x 512 block of N(0, 0.02^2) BF16 needs ~370 words, real model
@@ -38,8 +41,9 @@ constexpr uint32_t kDynLdsBudget = 48u * 1024u;       // dynamic LDS per workgro
 uint32_t slot_words_for(int layout) { return layout == 0 ? kSlotWords0 : layout == 1 ? kSlotWords1 : 0u; }
 
 // Layout 0: a workgroup owns G whole row groups, with G chosen so the grid is one residency round at two workgroups
-// per CU.  Tiles of at most 20 blocks get one half-wave per block (k_layout0); larger tiles are spread evenly over at
-// most 16 half-waves that each decode several blocks through two LDS slots (k_layout0_pipe).
+// per CU.  Tiles of at most 20 blocks get one half-wave per block (PIPE = false: every wave decodes at once, the most
+// latency hiding); larger tiles are spread evenly over at most 16 half-waves that each decode several blocks, one
+// round at a time, through two region buffers (PIPE = true).
 constexpr uint32_t kDynLdsPipe = 62u * 1024u;         // two such workgroups per CU next to their decode tables
 
 bool plan_layout0(const Shape &f, int mode, int ncu, LaunchPlan &p) {
@@ -63,7 +67,7 @@ bool plan_layout0(const Shape &f, int mode, int ncu, LaunchPlan &p) {
             lds = halves * 2u * slot * 4u + G * part;
             pipe = true;
         }
-        if (lds <= (pipe ? kDynLdsPipe : kDynLdsBudget)) {
+        if (lds <= kDynLdsPipe) {
             p.pipe = pipe;
             p.G = G;
             p.threads = 32u * halves;

@@ -25,15 +25,16 @@ template <> struct XRegs<false> { float f[16]; };
 
 // ---------------------------------------------------------------------------------------------------------------
 // Layout 0: lane L of block (rb, cb) owns columns cb*512 + 16L .. +15 of rows rb*8 .. rb*8+7, stream order row-major.
-// Loads are unconditional and unmasked: rows past M and columns past K16 read row 0 / column 0 instead, so a loop
-// that issues them keeps static wait counts and no select has to wait for the data.  Their products are garbage and
+// Raw-plane row of a lane (16 weights: word k holds weights 4k..4k+3).  Loads are unconditional and unmasked, so a
+// loop that issues them keeps static wait counts and no select waits for the data: rows past M read row M - 1, and
+// columns past K16 read into the next row (or the 512 slack bytes after the plane).  Those products are garbage and
 // are dropped: sums of lanes past K16 are zeroed (col_ok selects), rows past M are never stored.
 template <int ELEM>
 __device__ __forceinline__ uint4 raw_row0(const uint8_t *__restrict__ low, const Shape &f, uint32_t row, uint32_t col0, bool col_ok) {
     const bool ok = row < f.M && col_ok;
-    const uint64_t r = ok ? row : 0u, c = ok ? col0 : 0u;
-    if (ELEM == kElemFp8) return expand_nibbles(ldnt2(low + r * (f.K16 / 2) + c / 2));
-    return ldnt4(low + r * f.K16 + c);
+    const uint32_t r = ok ? row : 0u, c = ok ? col0 : 0u;
+    if (ELEM == kElemFp8) return expand_nibbles(ldnt2(low + (r * (f.K16 / 2) + c / 2)));
+    return ldnt4(low + (r * f.K16 + c));
 }
 
 template <bool XBF16>
@@ -55,6 +56,7 @@ __device__ __forceinline__ void load_x16(XRegs<XBF16> &x, const void *xp, uint32
 // Position of block t (0 <= t < G * CB) of a workgroup's tile for lane L.
 struct Coord0 {
     uint32_t g, cb, b, row0, col0;
+    uint32_t rb, rmax;          // raw-plane byte offsets of (row0, col0) and (M - 1, col0)
     bool col_ok;
 };
 __device__ __forceinline__ Coord0 coord0(uint32_t t, uint32_t rg0, const Shape &f, uint32_t L) {
@@ -66,7 +68,17 @@ __device__ __forceinline__ Coord0 coord0(uint32_t t, uint32_t rg0, const Shape &
     c.row0 = rb * kRows0;
     c.col0 = c.cb * kCols + L * 16;
     c.col_ok = c.col0 < f.K16;
+    c.rb = c.row0 * f.K16 + c.col0;                          // BF16: one byte per weight; fp8: halved below
+    c.rmax = (f.M - 1u) * f.K16 + c.col0;
     return c;
+}
+
+// Raw-plane row r of block c (see raw_row0 for the out-of-range rules); the row offset r * stride is uniform.
+template <int ELEM>
+__device__ __forceinline__ uint4 raw_row(const uint8_t *__restrict__ low, const Shape &f, const Coord0 &c, uint32_t r) {
+    const uint32_t off = min(c.rb + r * f.K16, c.rmax);
+    if (ELEM == kElemFp8) return expand_nibbles(ldnt2(low + off / 2));
+    return ldnt4(low + off);
 }
 
 // Weights of one window step for the accumulator / dequant output.
@@ -153,12 +165,12 @@ __device__ __forceinline__ float row0(Seq<ELEM> &S, const LutLds &s, const uint4
     float sum = 0.f;
 #pragma unroll
     for (int k = 0; k < 4; k++) {
-        const int32_t nm0 = S.nm;
+        const uint32_t s0 = S.s;
         const uint32_t *wp0 = S.wp;
         uint32_t e1, e2;
         S.fast_quad(s, e1, e2);
         if (__any((int)(e1 | e2) < 0)) {
-            S.nm = nm0;
+            S.s = s0;
             S.wp = wp0;
             S.reload();
             S.slow_quad(s, e1, e2);
@@ -210,8 +222,7 @@ __device__ __forceinline__ float rows0_ring(const LutLds &s, const uint32_t *wor
         }
         uint32_t pw[8];
         const float sum = row0<ELEM, MODE, XBF16>(S, s, ring[r & 3], x, pw);
-        ring[r & 3] = r < 4 ? raw_row0<ELEM>(a.low, f, c.row0 + r + 4, c.col0, c.col_ok)
-                            : raw_row0<ELEM>(a.low, f, nx.row0 + r - 4, nx.col0, nx.col_ok);
+        ring[r & 3] = r < 4 ? raw_row<ELEM>(a.low, f, c, r + 4) : raw_row<ELEM>(a.low, f, nx, r - 4);
         if (MODE == kDequant) store_row0<MODE>(a, f, valid ? c.row0 + r : f.M, c.col0, c.col_ok, pw);
         else acc[r] = c.col_ok ? sum : 0.f;
     }
@@ -230,7 +241,7 @@ __device__ __forceinline__ float rows0_global(const LutLds &s, const uint32_t *w
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll 1
     for (int r = 0; r < (int)kRows0; r++) {
-        const uint4 cur = raw_row0<ELEM>(a.low, f, c.row0 + r, c.col0, c.col_ok);
+        const uint4 cur = raw_row<ELEM>(a.low, f, c, r);
         uint32_t pw[8];
         const float sum = row0<ELEM, MODE, XBF16>(S, s, cur, x, pw);
         if (MODE == kDequant) {
@@ -284,7 +295,7 @@ __global__ void __launch_bounds__(1024) k_layout0(BlockArgs a) {
         lut_commit<kLutSeq>(s, Q, a.lut);
         uint4 raw[8];
 #pragma unroll
-        for (int r = 0; r < (int)kRows0; r++) raw[r] = raw_row0<ELEM>(a.low, f, c.row0 + r, c.col0, c.col_ok);
+        for (int r = 0; r < (int)kRows0; r++) raw[r] = raw_row<ELEM>(a.low, f, c, r);
         const bool fits = R.n16 * 4u <= cap;
         if (fits) bulk_commit(Bk, cur, R, tid, nth);
         __syncthreads();
@@ -298,7 +309,7 @@ __global__ void __launch_bounds__(1024) k_layout0(BlockArgs a) {
     } else {
         uint4 ring[4];
 #pragma unroll
-        for (int r = 0; r < 4; r++) ring[r] = raw_row0<ELEM>(a.low, f, c.row0 + r, c.col0, c.col_ok);
+        for (int r = 0; r < 4; r++) ring[r] = raw_row<ELEM>(a.low, f, c, r);
         Coord0 cn = coord0(min(t + H, tl), rg0, f, L);
         uint32_t n_n = a.hdr[(uint64_t)cn.b * kHdrBytes + L], base_n = a.bases[cn.b];
         Region Rn = region_of(a, B0 + min(H, tl), B0 + min(2u * H, nt), nb, mend);
@@ -323,7 +334,7 @@ __global__ void __launch_bounds__(1024) k_layout0(BlockArgs a) {
                 if (MODE != kDequant) load_x16<XBF16>(xn, a.x, cn.col0, cn.col_ok);
                 v = rows0_global<ELEM, MODE, XBF16>(s, (const uint32_t *)(a.data + base) + start, a, f, x, c, valid, L);
 #pragma unroll
-                for (int r = 0; r < 4; r++) ring[r] = raw_row0<ELEM>(a.low, f, cn.row0 + r, cn.col0, cn.col_ok);
+                for (int r = 0; r < 4; r++) ring[r] = raw_row<ELEM>(a.low, f, cn, r);
             }
             if (valid && MODE != kDequant && (L & 3) == 0) part[(c.g * kRows0 + (L >> 2)) * f.CB + c.cb] = v;
             if (k + 1u >= rounds) break;

@@ -236,67 +236,68 @@ struct Window {
 };
 
 // ---- bit cursor over an LDS-staged lane stream ----
-// P = bit position of the next code (0 = the MSB of the lane's word 0).  The cursor keeps nm = ~(P - 1), the word
-// pointer wp = lane + ((P - 1) >> 5) and the words A = wp[0], B = wp[1], C = wp[2]; the 32 bits from P are then
-// alignbit(A, B, nm) (the shift takes nm's low five bits, 31 - ((P - 1) & 31)).  An advance by c <= 24 bits moves
-// at most one word, exactly when c > (nm & 31): A, B <- B, C, and the new C is read for the step after next.  So no
-// read of stream words lies on the dependency chain of a step, which is
-//   window -> table read (kLutSeq encoding) -> shift -> table read -> add -> compare -> select -> window.
+// P = bit position of the next code (0 = the MSB of the lane's word 0).  The cursor keeps the word pointer
+// wp = lane + ((P - 1) >> 5), the words A = wp[0], B = wp[1], C = wp[2], and s = 31 - ((P - 1) & 31): the 32 bits
+// from P are then alignbit(A, B, s).  An advance by c <= 24 bits moves at most one word, exactly when c > s:
+// A, B <- B, C, and the new C is read for the step after next, so no read of stream words lies on the dependency chain
+// of a step:  window -> table read (kLutSeq encoding) -> shift -> table read -> add -> test -> select -> window.
 // The words may live in LDS (staged streams) or global memory (fallback).
 template <int ELEM>
 struct Seq {
     const uint32_t *wp;
-    int32_t nm;
+    uint32_t s;
     uint32_t A, B, C;
 
-    // At P = 0, P - 1 = -1 lies in word -1, whose value is never used: shift 0 selects B, and the first step always
-    // moves a word.  It is not read either (word -1 of a global stream may precede the allocation).
+    // At P = 0, P - 1 = -1 lies in word -1, whose value is never used: shift 0 selects B, and any advance then moves
+    // a word.  It is not read either (word -1 of a global stream may precede the allocation).
     __device__ __forceinline__ void init(const uint32_t *lane) {
         wp = lane - 1;
-        nm = 0;
+        s = 0;
         A = 0u; B = lane[0]; C = lane[1];
     }
-    __device__ __forceinline__ uint32_t window() const { return __builtin_amdgcn_alignbit(A, B, (uint32_t)nm); }
-    __device__ __forceinline__ void step(bool crossed, int32_t nm2) {
-        nm = nm2;
+    __device__ __forceinline__ uint32_t window() const { return __builtin_amdgcn_alignbit(A, B, s); }
+    // t = s - c as an 8-bit two's complement value in its low byte (higher bits are don't-care)
+    __device__ __forceinline__ void step(uint32_t t) {
+        const bool crossed = (t & 0x80u) != 0;
+        s = t & 31u;
         A = crossed ? B : A;
         B = crossed ? C : B;
         wp = crossed ? wp + 1 : wp;
         C = wp[2];
     }
-    // re-read the cached words after the position was reset (at P = 0 word -1 is replaced by word 0, see init)
-    __device__ __forceinline__ void reload() { A = wp[nm == 0 ? 1 : 0]; B = wp[1]; C = wp[2]; }
+    // re-read the cached words after the position was reset; A is dead when s = 0 (see init), so it is not read then
+    __device__ __forceinline__ void reload() { A = wp[s == 0 ? 1 : 0]; B = wp[1]; C = wp[2]; }
 
     // Four codes = two pairs from two table reads; e1 holds the exponent bytes of weights 0,1 in bytes 1,2 and e2
     // those of weights 2,3.  Correct only if neither entry has bit 31; otherwise the caller resets the position and
-    // redoes the step with slow_quad.
-    __device__ __forceinline__ void fast_quad(const LutLds &s, uint32_t &e1, uint32_t &e2) {
+    // redoes the step with slow_quad.  Byte 0 of e1 + e2 is 36 - c (kLutSeq), so e1 + e2 + s - 36 has s - c in its low
+    // byte (bytes 1-3 hold exponent sums and do not matter).
+    __device__ __forceinline__ void fast_quad(const LutLds &T, uint32_t &e1, uint32_t &e2) {
         const uint32_t hi = window();
-        e1 = lds_entry(s, (hi >> 18) & 0x3FFCu);
-        e2 = lds_entry(s, (hi >> (e1 & 31u)) & 0x3FFCu);               // the 12 bits after the first c1
-        const uint32_t db = (e1 + e2) & 0xFFu;                         // 36 - c, c = c1 + c2 (kLutSeq table)
-        step(db < 36u - ((uint32_t)nm & 31u), nm - 36 + (int32_t)db);
+        e1 = lds_entry(T, (hi >> 18) & 0x3FFCu);
+        e2 = lds_entry(T, (hi >> (e1 & 31u)) & 0x3FFCu);               // the 12 bits after the first c1
+        step(e1 + e2 + (s - 36u));
     }
 
     // one code by counting leading zeros: rank r < max -> r zeros, one, sign; BF16 escape -> 15 zeros, one, byte
-    __device__ __forceinline__ uint32_t slow_code(const LutLds &s) {
+    __device__ __forceinline__ uint32_t slow_code(const LutLds &T) {
         const uint32_t hi = window();
         uint32_t u = __clz((int)hi), b, c;
         if (ELEM == kElemFp8 || u < kMaxRankBf16) {
             u = u < 15u ? u : 15u;
-            b = (((hi >> (30u - u)) & 1u) << 7) | s.eor[u];
+            b = (((hi >> (30u - u)) & 1u) << 7) | T.eor[u];
             c = u + 2u;
         } else {
             b = (hi >> 8) & 0xFFu;
             c = 24u;
         }
-        step(c > ((uint32_t)nm & 31u), nm - (int32_t)c);
+        step(s - c);
         return b;
     }
-    __device__ __forceinline__ void slow_quad(const LutLds &s, uint32_t &e1, uint32_t &e2) {
+    __device__ __forceinline__ void slow_quad(const LutLds &T, uint32_t &e1, uint32_t &e2) {
         uint32_t bytes = 0;                                            // b3 b2 b1 b0 after four codes
 #pragma unroll 1
-        for (int k = 0; k < 4; k++) bytes = (bytes >> 8) | (slow_code(s) << 24);
+        for (int k = 0; k < 4; k++) bytes = (bytes >> 8) | (slow_code(T) << 24);
         e1 = (bytes << 8) & 0x00FFFF00u;
         e2 = (bytes >> 8) & 0x00FFFF00u;
     }
