@@ -47,8 +47,9 @@ def clone_weight(c):
     from nwc_amd.nwc_torch import NWCWeight
     d = NWCWeight.__new__(NWCWeight)
     d.__dict__.update(c.__dict__)
-    for k in ("data", "bases", "hdr", "lut", "low"):
-        setattr(d, k, getattr(c, k).clone())
+    for k in ("data", "bases", "hdr", "lut", "low", "_row_index"):
+        if getattr(c, k, None) is not None:
+            setattr(d, k, getattr(c, k).clone())
     return d
 
 
@@ -58,7 +59,9 @@ class Launch:
     def __init__(self, c, x, y):
         from nwc_amd.nwc_torch import _lib, _ptr
         self.fn = _lib.nwc_linear_xbf16
-        self.args = [_ptr(c.data), _ptr(c.bases), _ptr(c.hdr), _ptr(c.lut), _ptr(c.low), _ptr(x), None,
+        ri = c.row_index()
+        self.args = [_ptr(c.data), _ptr(c.bases), _ptr(c.hdr), _ptr(c.lut), _ptr(c.low),
+                     _ptr(ri) if ri is not None else None, _ptr(x), None,
                      _ptr(c.scale) if c.scale is not None else None, _ptr(y), ctypes.c_uint64(c.n),
                      ctypes.c_uint32(c.in_features), ctypes.c_int(c.code)]
 
@@ -138,7 +141,7 @@ def run_gpu(args):
             raise SystemExit(f"{name}: token path outside tolerance ({err:.3e})")
 
     sh = ctypes.c_void_p(stream.cuda_stream)
-    bytes_tok = sum(c.bytes + 2 * K + 2 * M for name, M, K, c, x, w in base) * LAYERS
+    bytes_tok = sum(c.token_bytes() + 2 * K + 2 * M for name, M, K, c, x, w in base) * LAYERS
     bf16_tok = sum(2 * M * K + 2 * K + 2 * M for name, M, K, *_ in base) * LAYERS
 
     # ---- per-launch medians (the reference kernbench's method) ----
@@ -148,8 +151,8 @@ def run_gpu(args):
         for i in range(10):
             L[i % LAYERS](sh)
         ms, _ = event_ms(lambda j: L[j](sh), args.runs, LAYERS)
-        per.append({"layer": name, "M": M, "K": K, "nwc_bytes": c.bytes, "nwc_us": ms * 1e3,
-                    "nwc_GBps": (c.bytes + 2 * K + 2 * M) / (ms * 1e-3) / 1e9})
+        per.append({"layer": name, "M": M, "K": K, "nwc_bytes": c.token_bytes(), "nwc_us": ms * 1e3,
+                    "nwc_GBps": (c.token_bytes() + 2 * K + 2 * M) / (ms * 1e-3) / 1e9})
 
     # ---- the timed sweep: one token = 144 launches, captured as a HIP graph ----
     def sweep():
@@ -228,7 +231,7 @@ def run_gpu(args):
     # ---- roofline of the dominant kernel: average launch time of back-to-back gate_up launches ----
     name, M, K, c, x, w = next(b for b in base if b[0] == DOMINANT)
     L = launches[name]
-    dom_bytes = c.bytes + 2 * K + 2 * M
+    dom_bytes = c.token_bytes() + 2 * K + 2 * M
     dom_ms = avg_launch_ms(lambda j: L[j](ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)), LAYERS, 4)
     sum_launch_us = LAYERS * sum(p["nwc_us"] for p in per)
     return {
@@ -300,7 +303,7 @@ def run_profile(args):
     for i in range(args.profile_launches):
         L[i % len(L)](sh)
     torch.cuda.synchronize()
-    print(f"{DOMINANT}: {args.profile_launches} launches, {c.bytes + 2 * K + 2 * M} algorithmic bytes each", flush=True)
+    print(f"{DOMINANT}: {args.profile_launches} launches, {c.token_bytes() + 2 * K + 2 * M} algorithmic bytes each", flush=True)
 
 
 def main():

@@ -61,11 +61,24 @@ int nwc_linear_bf16(void *stream, const uint8_t *data, const uint32_t *bases, co
                     uint16_t *y, uint64_t n, uint32_t block, uint32_t K, int elem);
 
 /* Token path with x as BF16 for every layout (layout 0: BF16 [K16]; layouts 1/2: BF16 [K32]), otherwise as
- * nwc_linear_bf16.  No counterpart in the reference, whose Python side converts x to fp32 for layout 0 with an
- * extra kernel (nwc_torch.py:238-239); callers that hold BF16 activations use this one. */
+ * nwc_linear_bf16.  row_index: the layout-0 row index from nwc_row_index, or NULL; with it, small matrices decode
+ * each block's rows 0-3 and 4-7 on two half-waves at once (same results).  No counterpart in the reference, whose
+ * Python side converts x to fp32 for layout 0 with an extra kernel (nwc_torch.py:238-239); callers that hold BF16
+ * activations use this one. */
 int nwc_linear_xbf16(void *stream, const uint8_t *data, const uint32_t *bases, const uint8_t *hdr, const uint32_t *tab,
-                     const uint8_t *low, const uint16_t *x, const uint16_t *bias, const float *scale, uint16_t *y,
-                     uint64_t n, uint32_t K, int elem);
+                     const uint8_t *low, const uint16_t *row_index, const uint16_t *x, const uint16_t *bias,
+                     const float *scale, uint16_t *y, uint64_t n, uint32_t K, int elem);
+
+/* Layout-0 row index of a matrix: row_index[(b * 3 + j) * 32 + L] = the bit position, from lane L's first stream word
+ * of block b, where row 2 (j + 1) begins (uint16 [blocks x 3 x 32], 192 bytes per block).  Derived from the stored
+ * tensors (it is not part of the format), once per matrix; -1 for layouts 1/2 or a bad shape.  No counterpart in
+ * the reference. */
+int nwc_row_index(void *stream, const uint8_t *data, const uint32_t *bases, const uint8_t *hdr, const uint32_t *tab,
+                  const uint8_t *low, uint16_t *row_index, uint64_t n, uint32_t K, int elem);
+
+/* Half-waves per block that nwc_linear_xbf16 would use on the current device (1, or 2 with a row index), for byte
+ * accounting; -1 for a bad shape.  No counterpart in the reference. */
+int nwc_token_split(uint64_t n, uint32_t K, int elem, int with_row_index);
 
 /* Rows ids[0..n_ids) -> BF16 [n_ids x K16] (embedding lookup from the compressed matrix); ids outside [0, M) leave
  * their output row untouched, as in the reference.  0 for n_ids == 0.  Replaces nwc_ops.cu:1143. */

@@ -46,19 +46,22 @@ uint32_t slot_words_for(int layout) { return layout == 0 ? kSlotWords0 : layout 
 // round at a time, through two region buffers (PIPE = true).
 constexpr uint32_t kDynLdsPipe = 62u * 1024u;         // two such workgroups per CU next to their decode tables
 
-bool plan_layout0(const Shape &f, int mode, int ncu, LaunchPlan &p) {
+bool plan_layout0(const Shape &f, int mode, int ncu, bool index, LaunchPlan &p) {
     p = LaunchPlan{};
     p.layout = 0;
+    const bool rows = mode == kToken || mode == kF32;
     const uint32_t CB = f.CB, groups = f.groups(), slot = kSlotWords0;
-    const uint32_t part = mode == kDequant ? 0u : kRows0 * CB * 4u;     // row-sum bytes per row group
+    const uint32_t part = rows ? kRows0 * CB * 4u : 0u;                // row-sum bytes per row group
     uint32_t G = std::max(1u, (groups + 2u * (uint32_t)ncu - 1u) / (2u * (uint32_t)ncu));
     for (;; G--) {
         const uint32_t blocks = G * CB;
-        uint32_t halves, lds;
+        uint32_t halves, lds, split = 1;
         bool pipe;
         if (blocks <= 20) {
-            halves = (blocks + 1u) & ~1u;
-            lds = halves * slot * 4u + G * part;
+            // with the row index, two half-waves share a block (rows 0-3 / 4-7) while the tile stays <= 20 half-waves
+            split = index && rows && 2u * blocks <= 20u ? 2u : 1u;
+            halves = split == 2u ? 2u * blocks : (blocks + 1u) & ~1u;
+            lds = (halves / split) * slot * 4u + G * part;
             pipe = false;
         } else {
             const uint32_t rounds = (blocks + 15u) / 16u;
@@ -69,6 +72,7 @@ bool plan_layout0(const Shape &f, int mode, int ncu, LaunchPlan &p) {
         }
         if (lds <= kDynLdsPipe) {
             p.pipe = pipe;
+            p.split = split;
             p.G = G;
             p.threads = 32u * halves;
             p.grid = (groups + G - 1u) / G;
@@ -82,8 +86,8 @@ bool plan_layout0(const Shape &f, int mode, int ncu, LaunchPlan &p) {
 // Layouts 1/2: workgroup tile = G whole row groups, one block per half-wave where the LDS budget allows.  Prefer at
 // least two workgroups per CU (small matrices spread over the whole chip), at most 32 blocks (16 waves) per
 // workgroup, and an even block count so both halves of every wave have a block.
-bool plan_blocks(const Shape &f, int layout, int mode, int ncu, LaunchPlan &p) {
-    if (layout == 0) return plan_layout0(f, mode, ncu, p);
+bool plan_blocks(const Shape &f, int layout, int mode, int ncu, bool index, LaunchPlan &p) {
+    if (layout == 0) return plan_layout0(f, mode, ncu, index, p);
     p = LaunchPlan{};
     p.layout = layout;
     const uint32_t CB = f.CB, groups = f.groups(), slot = slot_words_for(layout);
@@ -111,14 +115,14 @@ bool plan_blocks(const Shape &f, int layout, int mode, int ncu, LaunchPlan &p) {
 
 int run_blocks(int mode, bool xbf16, hipStream_t st, const uint8_t *data, const uint32_t *bases, const uint8_t *hdr,
                const uint32_t *tab, const uint8_t *low, const void *x, const uint16_t *bias, const float *scale, void *out,
-               uint64_t n, uint32_t K, int elem) {
+               uint64_t n, uint32_t K, int elem, const uint16_t *aux = nullptr) {
     const int ncu = current_cus();
     if (ncu <= 0) return (int)hipErrorNoDevice;
     const int layout = elem_layout(elem), t = elem_type(elem);
     const Shape f((uint32_t)(n / K), K, layout);
     LaunchPlan p;
-    if (!plan_blocks(f, layout, mode, ncu, p)) return -1;
-    BlockArgs a{data, bases, hdr, tab, low, x, bias, scale, out, f.M, f.K, p.G, slot_words_for(layout)};
+    if (!plan_blocks(f, layout, mode, ncu, aux != nullptr && layout == 0, p)) return -1;
+    BlockArgs a{data, bases, hdr, tab, low, x, bias, scale, out, aux, f.M, f.K, p.G, slot_words_for(layout)};
     return layout == 2 ? launch_fixed(p, t, mode, xbf16, a, st) : launch_prefix(p, t, mode, xbf16, a, st);
 }
 
@@ -148,10 +152,28 @@ extern "C" int nwc_linear_bf16(void *stream, const uint8_t *data, const uint32_t
 }
 
 extern "C" int nwc_linear_xbf16(void *stream, const uint8_t *data, const uint32_t *bases, const uint8_t *hdr, const uint32_t *tab,
-                                const uint8_t *low, const uint16_t *x, const uint16_t *bias, const float *scale, uint16_t *y,
-                                uint64_t n, uint32_t K, int elem) {
+                                const uint8_t *low, const uint16_t *row_index, const uint16_t *x, const uint16_t *bias,
+                                const float *scale, uint16_t *y, uint64_t n, uint32_t K, int elem) {
     if (!shape_ok(n, kBlock, K, elem)) return -1;
-    return run_blocks(kToken, true, (hipStream_t)stream, data, bases, hdr, tab, low, x, bias, scale, y, n, K, elem);
+    return run_blocks(kToken, true, (hipStream_t)stream, data, bases, hdr, tab, low, x, bias, scale, y, n, K, elem,
+                      elem_layout(elem) == 0 ? row_index : nullptr);
+}
+
+extern "C" int nwc_row_index(void *stream, const uint8_t *data, const uint32_t *bases, const uint8_t *hdr, const uint32_t *tab,
+                             const uint8_t *low, uint16_t *row_index, uint64_t n, uint32_t K, int elem) {
+    if (!shape_ok(n, kBlock, K, elem) || elem_layout(elem) != 0) return -1;
+    return run_blocks(kRowIndex, true, (hipStream_t)stream, data, bases, hdr, tab, low, nullptr, nullptr, nullptr, row_index,
+                      n, K, elem);
+}
+
+extern "C" int nwc_token_split(uint64_t n, uint32_t K, int elem, int with_row_index) {
+    if (!shape_ok(n, kBlock, K, elem)) return -1;
+    const int ncu = current_cus();
+    if (ncu <= 0) return (int)hipErrorNoDevice;
+    const Shape f((uint32_t)(n / K), K, elem_layout(elem));
+    LaunchPlan p;
+    if (!plan_blocks(f, elem_layout(elem), kToken, ncu, with_row_index != 0 && elem_layout(elem) == 0, p)) return -1;
+    return elem_layout(elem) == 0 ? (int)p.split : 1;
 }
 
 extern "C" int nwc_gather(void *stream, const uint8_t *data, const uint32_t *bases, const uint8_t *hdr, const uint32_t *tab,

@@ -85,7 +85,9 @@ __device__ __forceinline__ uint4 raw_row(const uint8_t *__restrict__ low, const 
 template <int MODE, bool XBF16>
 __device__ __forceinline__ void use_quad(uint32_t e1, uint32_t e2, uint32_t rk, int k, const XRegs<XBF16> &x, float &sum,
                                          uint32_t pw[8]) {
-    if constexpr (MODE == kDequant) {
+    if constexpr (MODE == kRowIndex) {
+        (void)e1; (void)e2; (void)rk; (void)k; (void)x; (void)sum; (void)pw;
+    } else if constexpr (MODE == kDequant) {
         pw[2 * k] = perm(e1, rk, kSelPair0);
         pw[2 * k + 1] = perm(e2, rk, kSelPair2);
     } else if constexpr (XBF16) {
@@ -179,27 +181,33 @@ __device__ __forceinline__ float row0(Seq<ELEM> &S, const LutLds &s, const uint4
         // consume each step's weights before the next decode step (otherwise the compiler sinks every dot product to
         // the end of the unrolled block and keeps all decoded words live)
         if (MODE == kDequant) asm volatile("" : "+v"(pw[2 * k]), "+v"(pw[2 * k + 1]));
-        else asm volatile("" : "+v"(sum));
+        else if (MODE != kRowIndex) asm volatile("" : "+v"(sum));
     }
     return sum;
 }
 
-// The eight rows of one layout-0 block for one lane, decoded from LDS with all raw-plane rows already requested.
-// Returns the row sums reduced over the half-wave (lane 4r holds row r) or, for dequantization, stores the rows.
-template <int ELEM, int MODE, bool XBF16>
-__device__ __forceinline__ float rows0(const LutLds &s, const uint32_t *words, const BlockArgs &a, const Shape &f,
-                                       const XRegs<XBF16> &x, const uint4 raw[8], const Coord0 &c, uint32_t L) {
+// Rows r0 .. r0 + NR - 1 of one layout-0 block for one lane, decoded from LDS starting at bit position P0 of the lane's
+// stream, with those raw-plane rows already requested.  Returns the row sums reduced over the half-wave (NR = 8: lane
+// 4r holds row r0 + r; NR = 4: lane 8r) or, for dequantization, stores the rows; MODE kRowIndex records the row
+// index (positions of rows 2, 4, 6) instead.  Fully unrolled: every row's raw bytes live in their own registers.
+template <int ELEM, int MODE, bool XBF16, int NR>
+__device__ __forceinline__ float rowsN(const LutLds &s, const uint32_t *lane, uint32_t P0, const BlockArgs &a, const Shape &f,
+                                       const XRegs<XBF16> &x, const uint4 raw[NR], const Coord0 &c, uint32_t r0, uint32_t L) {
     Seq<ELEM> S;
-    S.init(words);
-    float acc[8];
+    S.init_at(lane, P0);
+    float acc[NR];
 #pragma unroll
-    for (int r = 0; r < (int)kRows0; r++) {
+    for (int r = 0; r < NR; r++) {
+        if (MODE == kRowIndex && r > 0 && (r & 1) == 0)
+            ((uint16_t *)a.out)[((uint64_t)c.b * kRowIndexSplits + (r >> 1) - 1) * kLanes + L] = (uint16_t)S.position(lane);
         uint32_t pw[8];
         const float sum = row0<ELEM, MODE, XBF16>(S, s, raw[r], x, pw);
-        if (MODE == kDequant) store_row0<MODE>(a, f, c.row0 + r, c.col0, c.col_ok, pw);
+        if (MODE == kDequant) store_row0<MODE>(a, f, c.row0 + r0 + r, c.col0, c.col_ok, pw);
         else acc[r] = c.col_ok ? sum : 0.f;
     }
-    return MODE == kDequant ? 0.f : reduce8_transposed(acc, L);
+    if (MODE == kDequant || MODE == kRowIndex) return 0.f;
+    if constexpr (NR == 8) return reduce8_transposed(acc, L);
+    else return reduce4_transposed(acc, L);
 }
 
 // rows0 for the pipelined kernel.  The raw-plane rows go through a ring of four registers (row r + 4 of this block
@@ -218,15 +226,18 @@ __device__ __forceinline__ float rows0_ring(const LutLds &s, const uint32_t *wor
     for (int r = 0; r < (int)kRows0; r++) {
         if (r == 4) {
             bulk_issue(Bk, a.data, Rn, tid, nth);
-            if (MODE != kDequant) load_x16<XBF16>(xn, a.x, nx.col0, nx.col_ok);
+            if (MODE == kToken || MODE == kF32) load_x16<XBF16>(xn, a.x, nx.col0, nx.col_ok);
         }
+        if (MODE == kRowIndex && r > 0 && (r & 1) == 0 && valid)
+            ((uint16_t *)a.out)[((uint64_t)c.b * kRowIndexSplits + (r >> 1) - 1) * kLanes + L] = (uint16_t)S.position(words);
         uint32_t pw[8];
         const float sum = row0<ELEM, MODE, XBF16>(S, s, ring[r & 3], x, pw);
-        ring[r & 3] = r < 4 ? raw_row<ELEM>(a.low, f, c, r + 4) : raw_row<ELEM>(a.low, f, nx, r - 4);
+        if (MODE != kRowIndex)
+            ring[r & 3] = r < 4 ? raw_row<ELEM>(a.low, f, c, r + 4) : raw_row<ELEM>(a.low, f, nx, r - 4);
         if (MODE == kDequant) store_row0<MODE>(a, f, valid ? c.row0 + r : f.M, c.col0, c.col_ok, pw);
         else acc[r] = c.col_ok ? sum : 0.f;
     }
-    return MODE == kDequant ? 0.f : reduce8_transposed(acc, L);
+    return MODE == kDequant || MODE == kRowIndex ? 0.f : reduce8_transposed(acc, L);
 }
 
 // The same for a block of a round whose streams do not fit the region buffer: decoded straight from global memory
@@ -241,7 +252,9 @@ __device__ __forceinline__ float rows0_global(const LutLds &s, const uint32_t *w
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll 1
     for (int r = 0; r < (int)kRows0; r++) {
-        const uint4 cur = raw_row<ELEM>(a.low, f, c, r);
+        if (MODE == kRowIndex && r > 0 && (r & 1) == 0 && valid)
+            ((uint16_t *)a.out)[((uint64_t)c.b * kRowIndexSplits + (r >> 1) - 1) * kLanes + L] = (uint16_t)S.position(words);
+        const uint4 cur = MODE == kRowIndex ? make_uint4(0u, 0u, 0u, 0u) : raw_row<ELEM>(a.low, f, c, r);
         uint32_t pw[8];
         const float sum = row0<ELEM, MODE, XBF16>(S, s, cur, x, pw);
         if (MODE == kDequant) {
@@ -252,7 +265,34 @@ __device__ __forceinline__ float rows0_global(const LutLds &s, const uint32_t *w
             acc[kRows0 - 1] = c.col_ok ? sum : 0.f;
         }
     }
-    return MODE == kDequant ? 0.f : reduce8_transposed(acc, L);
+    return MODE == kDequant || MODE == kRowIndex ? 0.f : reduce8_transposed(acc, L);
+}
+
+// rowsN for a half-wave share of a block whose round does not fit the region buffer: from global memory, rolled.
+template <int ELEM, int MODE, bool XBF16, int NR>
+__device__ __forceinline__ float rowsN_global(const LutLds &s, const uint32_t *lane, uint32_t P0, const BlockArgs &a,
+                                              const Shape &f, const XRegs<XBF16> &x, const Coord0 &c, uint32_t r0, uint32_t L) {
+    Seq<ELEM> S;
+    S.init_at(lane, P0);
+    float acc[NR];
+#pragma unroll
+    for (int i = 0; i < NR; i++) acc[i] = 0.f;
+#pragma unroll 1
+    for (int r = 0; r < NR; r++) {
+        const uint4 cur = raw_row<ELEM>(a.low, f, c, r0 + r);
+        uint32_t pw[8];
+        const float sum = row0<ELEM, MODE, XBF16>(S, s, cur, x, pw);
+        if (MODE == kDequant) {
+            store_row0<MODE>(a, f, c.row0 + r0 + r, c.col0, c.col_ok, pw);
+        } else {
+#pragma unroll
+            for (int i = 0; i < NR - 1; i++) acc[i] = acc[i + 1];
+            acc[NR - 1] = c.col_ok ? sum : 0.f;
+        }
+    }
+    if (MODE == kDequant || MODE == kRowIndex) return 0.f;
+    if constexpr (NR == 8) return reduce8_transposed(acc, L);
+    else return reduce4_transposed(acc, L);
 }
 
 // Layout 0.  A workgroup owns G whole row groups (nt = G * CB blocks) and works through them in rounds of H blocks,
@@ -262,13 +302,17 @@ __device__ __forceinline__ float rows0_global(const LutLds &s, const uint32_t *w
 //   PIPE = true: two region buffers; while round k decodes, round k + 1's streams, raw rows (four-register ring) and
 //     activations are in flight and round k + 2's bounds and header bytes are read, so after the first round no step
 //     waits on global memory.  One barrier per round publishes the next region.
-template <int ELEM, int MODE, bool XBF16, bool PIPE>
+template <int ELEM, int MODE, bool XBF16, bool PIPE, int NR>
 __global__ void __launch_bounds__(1024) k_layout0(BlockArgs a) {
+    static_assert(NR == 8 || (NR == 4 && !PIPE), "row splits only in the single-round kernel");
+    constexpr uint32_t SP = kRows0 / NR;                      // half-waves per block
+    constexpr bool ROWS = MODE == kToken || MODE == kF32;     // modes that keep row sums
     __shared__ LutLds s;
     extern __shared__ uint32_t dyn[];
     const uint32_t tid = threadIdx.x, nth = blockDim.x, L = tid & 31;
     const uint32_t hw = tid >> 5, H = nth >> 5;
-    const uint32_t cap = a.slot_words * H;                    // words per region buffer
+    const uint32_t HB = H / SP;                               // blocks per round
+    const uint32_t cap = a.slot_words * HB;                   // words per region buffer
     uint32_t *cur = dyn, *nxt = dyn + cap;
     float *part = (float *)(dyn + (PIPE ? 2u : 1u) * cap);
     const Shape f(a.M, a.K, 0);
@@ -279,37 +323,42 @@ __global__ void __launch_bounds__(1024) k_layout0(BlockArgs a) {
     const uint32_t mend = B0 + nt == nb ? matrix_end(a, nb) : 0u;
     // request order: region bounds and table first, then the stream copy (which needs the bounds), then the raw rows
     // and activations; loads complete in order, so each wait below covers only what it needs
-    Region R = region_of(a, B0, B0 + min(H, nt), nb, mend);
+    Region R = region_of(a, B0, B0 + min(HB, nt), nb, mend);
     LutLoad Q;
     lut_issue(Q, a.lut);
-    uint32_t t = hw;
+    uint32_t t = hw / SP;
+    const uint32_t r0 = (hw % SP) * NR;                       // first row of this half-wave's share of the block
     Coord0 c = coord0(min(t, tl), rg0, f, L);
     uint32_t n = a.hdr[(uint64_t)c.b * kHdrBytes + L], base = a.bases[c.b];
+    const uint32_t P0 = r0 ? a.aux[((uint64_t)c.b * kRowIndexSplits + (r0 >> 1) - 1) * kLanes + L] : 0u;
     Bulk Bk;
     bulk_issue(Bk, a.data, R, tid, nth);
     XRegs<XBF16> x;
-    if (MODE != kDequant) load_x16<XBF16>(x, a.x, c.col0, c.col_ok);
+    if (ROWS) load_x16<XBF16>(x, a.x, c.col0, c.col_ok);
 
     if constexpr (!PIPE) {
         // the table is stored before the raw rows are requested, so its registers are free for them
         lut_commit<kLutSeq>(s, Q, a.lut);
-        uint4 raw[8];
+        uint4 raw[NR];
 #pragma unroll
-        for (int r = 0; r < (int)kRows0; r++) raw[r] = raw_row<ELEM>(a.low, f, c, r);
+        for (int r = 0; r < NR; r++) raw[r] = MODE == kRowIndex ? make_uint4(0u, 0u, 0u, 0u) : raw_row<ELEM>(a.low, f, c, r0 + r);
         const bool fits = R.n16 * 4u <= cap;
         if (fits) bulk_commit(Bk, cur, R, tid, nth);
         __syncthreads();
         if (t < nt) {
             const uint32_t start = c.col_ok ? half_scan_incl(n, L) - n : 0u;
             float v;
-            if (fits) v = rows0<ELEM, MODE, XBF16>(s, cur + ((base - R.lo16) >> 2) + start, a, f, x, raw, c, L);
-            else v = rows0_global<ELEM, MODE, XBF16>(s, (const uint32_t *)(a.data + base) + start, a, f, x, c, true, L);
-            if (MODE != kDequant && (L & 3) == 0) part[(c.g * kRows0 + (L >> 2)) * f.CB + c.cb] = v;
+            if (fits) v = rowsN<ELEM, MODE, XBF16, NR>(s, cur + ((base - R.lo16) >> 2) + start, P0, a, f, x, raw, c, r0, L);
+            else if constexpr (NR == 8)
+                v = rows0_global<ELEM, MODE, XBF16>(s, (const uint32_t *)(a.data + base) + start, a, f, x, c, true, L);
+            else
+                v = rowsN_global<ELEM, MODE, XBF16, NR>(s, (const uint32_t *)(a.data + base) + start, P0, a, f, x, c, r0, L);
+            if (ROWS && (L & (4u * SP - 1u)) == 0) part[(c.g * kRows0 + r0 + L / (4u * SP)) * f.CB + c.cb] = v;
         }
     } else {
         uint4 ring[4];
 #pragma unroll
-        for (int r = 0; r < 4; r++) ring[r] = raw_row<ELEM>(a.low, f, c, r);
+        for (int r = 0; r < 4; r++) ring[r] = MODE == kRowIndex ? make_uint4(0u, 0u, 0u, 0u) : raw_row<ELEM>(a.low, f, c, r);
         Coord0 cn = coord0(min(t + H, tl), rg0, f, L);
         uint32_t n_n = a.hdr[(uint64_t)cn.b * kHdrBytes + L], base_n = a.bases[cn.b];
         Region Rn = region_of(a, B0 + min(H, tl), B0 + min(2u * H, nt), nb, mend);
@@ -331,12 +380,12 @@ __global__ void __launch_bounds__(1024) k_layout0(BlockArgs a) {
                                                   Rn, xn, tid, nth, L);
             } else {
                 bulk_issue(Bk, a.data, Rn, tid, nth);
-                if (MODE != kDequant) load_x16<XBF16>(xn, a.x, cn.col0, cn.col_ok);
+                if (ROWS) load_x16<XBF16>(xn, a.x, cn.col0, cn.col_ok);
                 v = rows0_global<ELEM, MODE, XBF16>(s, (const uint32_t *)(a.data + base) + start, a, f, x, c, valid, L);
 #pragma unroll
-                for (int r = 0; r < 4; r++) ring[r] = raw_row<ELEM>(a.low, f, cn, r);
+                for (int r = 0; r < 4; r++) ring[r] = MODE == kRowIndex ? make_uint4(0u, 0u, 0u, 0u) : raw_row<ELEM>(a.low, f, cn, r);
             }
-            if (valid && MODE != kDequant && (L & 3) == 0) part[(c.g * kRows0 + (L >> 2)) * f.CB + c.cb] = v;
+            if (valid && ROWS && (L & 3) == 0) part[(c.g * kRows0 + (L >> 2)) * f.CB + c.cb] = v;
             if (k + 1u >= rounds) break;
             if (Rn.n16 * 4u <= cap) bulk_commit(Bk, nxt, Rn, tid, nth);
             __syncthreads();                                     // region k + 1 visible; region k free
@@ -345,7 +394,7 @@ __global__ void __launch_bounds__(1024) k_layout0(BlockArgs a) {
             base = base_n;
             R = Rn;
             Rn = Rnn;
-            if (MODE != kDequant) x = xn;
+            if (ROWS) x = xn;
             c = cn;
             cn = cnn;
             n_n = n_nn;
@@ -353,7 +402,7 @@ __global__ void __launch_bounds__(1024) k_layout0(BlockArgs a) {
             t += H;
         }
     }
-    if (MODE != kDequant) finish_rows<MODE>(a, part, rg0 * kRows0, ng * kRows0, f.CB);
+    if (ROWS) finish_rows<MODE>(a, part, rg0 * kRows0, ng * kRows0, f.CB);
 }
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -567,21 +616,27 @@ __global__ void __launch_bounds__(256) k_gather1(GatherArgs a) {
 template <int ELEM, int MODE, bool XBF16>
 static int launch_prefix_t(const LaunchPlan &p, const BlockArgs &a, hipStream_t st) {
     if (p.layout == 0 && p.pipe)
-        hipLaunchKernelGGL((k_layout0<ELEM, MODE, XBF16, true>), dim3(p.grid), dim3(p.threads), p.lds, st, a);
+        hipLaunchKernelGGL((k_layout0<ELEM, MODE, XBF16, true, 8>), dim3(p.grid), dim3(p.threads), p.lds, st, a);
+    else if (p.layout == 0 && p.split == 2 && (MODE == kToken || MODE == kF32))
+        hipLaunchKernelGGL((k_layout0<ELEM, MODE, XBF16, false, 4>), dim3(p.grid), dim3(p.threads), p.lds, st, a);
     else if (p.layout == 0)
-        hipLaunchKernelGGL((k_layout0<ELEM, MODE, XBF16, false>), dim3(p.grid), dim3(p.threads), p.lds, st, a);
-    else
+        hipLaunchKernelGGL((k_layout0<ELEM, MODE, XBF16, false, 8>), dim3(p.grid), dim3(p.threads), p.lds, st, a);
+    else if constexpr (MODE != kRowIndex)
         hipLaunchKernelGGL((k_layout1<ELEM, MODE, XBF16>), dim3(p.grid), dim3(p.threads), p.lds, st, a);
+    else
+        return -1;
     return (int)hipGetLastError();
 }
 
 int launch_prefix(const LaunchPlan &p, int elem_t, int mode, bool xbf16, const BlockArgs &a, hipStream_t st) {
     if (elem_t == kElemFp8) {
         if (mode == kDequant) return launch_prefix_t<kElemFp8, kDequant, true>(p, a, st);
+        if (mode == kRowIndex) return launch_prefix_t<kElemFp8, kRowIndex, true>(p, a, st);
         if (mode == kF32) return launch_prefix_t<kElemFp8, kF32, false>(p, a, st);
         return xbf16 ? launch_prefix_t<kElemFp8, kToken, true>(p, a, st) : launch_prefix_t<kElemFp8, kToken, false>(p, a, st);
     }
     if (mode == kDequant) return launch_prefix_t<kElemBf16, kDequant, true>(p, a, st);
+    if (mode == kRowIndex) return launch_prefix_t<kElemBf16, kRowIndex, true>(p, a, st);
     if (mode == kF32) return launch_prefix_t<kElemBf16, kF32, false>(p, a, st);
     return xbf16 ? launch_prefix_t<kElemBf16, kToken, true>(p, a, st) : launch_prefix_t<kElemBf16, kToken, false>(p, a, st);
 }

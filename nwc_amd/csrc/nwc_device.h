@@ -85,6 +85,23 @@ __device__ __forceinline__ float reduce8_transposed(float acc[8], uint32_t L) {
     return v;
 }
 
+// The same for 4 row sums: afterwards lane L with (L & 7) == 0 holds the sum of row L >> 3.
+__device__ __forceinline__ float reduce4_transposed(float acc[4], uint32_t L) {
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const bool up = L & 16;
+        float send = up ? acc[i] : acc[i + 2], keep = up ? acc[i + 2] : acc[i];
+        acc[i] = keep + xor_f<16>(send);
+    }
+    const bool up = L & 8;
+    float send = up ? acc[0] : acc[1], keep = up ? acc[1] : acc[0];
+    float v = keep + xor_f<8>(send);
+    v += xor_f<4>(v);
+    v += xor_f<2>(v);
+    v += xor_f<1>(v);
+    return v;
+}
+
 // ---- decode table in LDS ----
 // The stored 4096-word LUT is re-encoded once per workgroup.  Entries that are not two complete codes get bit 31 (slow
 // path); for the others byte 0 (c = bits of both codes, 4..12) becomes
@@ -255,6 +272,15 @@ struct Seq {
         s = 0;
         A = 0u; B = lane[0]; C = lane[1];
     }
+    // start at bit position P of the lane's stream (any P >= 0; P = 0 is init's case)
+    __device__ __forceinline__ void init_at(const uint32_t *lane, uint32_t P) {
+        const int32_t m = (int32_t)P - 1;
+        wp = lane + (m >> 5);
+        s = 31u - ((uint32_t)m & 31u);
+        reload();
+    }
+    // the bit position of the next code
+    __device__ __forceinline__ uint32_t position(const uint32_t *lane) const { return (uint32_t)(wp - lane) * 32u + 32u - s; }
     __device__ __forceinline__ uint32_t window() const { return __builtin_amdgcn_alignbit(A, B, s); }
     // t = s - c as an 8-bit two's complement value in its low byte (higher bits are don't-care)
     __device__ __forceinline__ void step(uint32_t t) {
@@ -344,7 +370,8 @@ struct BlockArgs {
     const void *x;          // fp32 or BF16 activations
     const uint16_t *bias;   // BF16 [M] or null
     const float *scale;     // fp32 [M] or null
-    void *out;              // token: BF16 y [M]; fp32 path: y [M]; dequant: BF16 [M x K16]
+    void *out;              // token: BF16 y [M]; fp32 path: y [M]; dequant: BF16 [M x K16]; row index: u16 [nb x 3 x 32]
+    const uint16_t *aux;    // layout 0 row index (bit positions of rows 2, 4, 6 per lane and block) or null
     uint32_t M, K;
     uint32_t G;             // row groups per workgroup
     uint32_t slot_words;    // LDS words per half-wave for a staged block (layouts 0/1)
@@ -363,7 +390,12 @@ struct GatherArgs {
     uint32_t slot_words;
 };
 
-enum Mode { kToken = 0, kDequant = 1, kF32 = 2 };
+enum Mode { kToken = 0, kDequant = 1, kF32 = 2, kRowIndex = 3 };
+
+// Layout-0 row index: for block b, lane L and j = 0..2, the bit position (from the lane's first word) where row
+// 2 (j + 1) of the lane's stream begins, at aux[(b * 3 + j) * 32 + L].  Built once per matrix (MODE kRowIndex); it lets
+// several half-waves decode one block's rows in parallel.
+constexpr uint32_t kRowIndexSplits = 3;
 
 // Workgroup epilogue of the token / fp32 paths: rows of the tile summed over the column blocks (ascending),
 // times scale, plus bias, rounded to BF16 (token) or written as fp32.

@@ -6,7 +6,8 @@ namespace nwc {
 
 struct LaunchPlan {
     int layout;
-    bool pipe;              // layout 0: two LDS slots per half-wave, next block prefetched (k_layout0_pipe)
+    bool pipe;              // layout 0: rounds through two region buffers, the next round prefetched
+    uint32_t split;         // layout 0: half-waves per block (1, or 2 with the row index)
     uint32_t grid, threads, lds, G;
 };
 

@@ -58,7 +58,10 @@ _lib.nwc_dequant.restype = I32; _lib.nwc_dequant.argtypes = [P, P, P, P, P, P, P
 _lib.nwc_linear_bf16.restype = I32
 _lib.nwc_linear_bf16.argtypes = [P, P, P, P, P, P, P, P, P, P, P, U64, U32, U32, I32]
 _lib.nwc_linear_xbf16.restype = I32
-_lib.nwc_linear_xbf16.argtypes = [P, P, P, P, P, P, P, P, P, P, U64, U32, I32]
+_lib.nwc_linear_xbf16.argtypes = [P, P, P, P, P, P, P, P, P, P, P, U64, U32, I32]
+_lib.nwc_row_index.restype = I32; _lib.nwc_row_index.argtypes = [P, P, P, P, P, P, P, U64, U32, I32]
+_lib.nwc_token_split.restype = I32; _lib.nwc_token_split.argtypes = [U64, U32, I32, I32]
+ROW_INDEX = os.environ.get("NWC_ROW_INDEX", "1") != "0"   # layout 0: build the row index for the token path
 _lib.nwc_gather.restype = I32; _lib.nwc_gather.argtypes = [P, P, P, P, P, P, P, U32, P, U64, U32, U32, I32]
 _lib.nwc_ref_fp8.restype = I32; _lib.nwc_ref_fp8.argtypes = [P, P, P, P, P, U64, U32]
 _lib.nwc_setup.restype = I32; _lib.nwc_setup.argtypes = []
@@ -261,6 +264,28 @@ class NWCWeight:
             raise RuntimeError(f"nwc_matvec HIP error {err}")
         return y if self.scale is None else y * self.scale
 
+    def row_index(self):
+        """Layout-0 row index (uint16 [blocks x 3 x 32], built on the GPU on first use; not part of the format): lets
+        the token kernel decode a block's rows 0-3 and 4-7 on two half-waves.  None for layouts 1/2 or NWC_ROW_INDEX=0."""
+        if self.layout != 0 or not ROW_INDEX:
+            return None
+        ri = getattr(self, "_row_index", None)
+        if ri is None:
+            _need_gpu(self.data)
+            ri = torch.empty(self.bases.numel() * 3 * LANES, dtype=torch.int16, device=self.data.device)
+            err = _lib.nwc_row_index(_stream(), _ptr(self.data), _ptr(self.bases), _ptr(self.hdr), _ptr(self.lut),
+                                     _ptr(self.low), _ptr(ri), self.n, self.in_features, self.code)
+            if err:
+                raise RuntimeError(f"nwc_row_index error {err}")
+            self._row_index = ri
+        return ri
+
+    def token_bytes(self):
+        """Algorithmic bytes one token-path call reads: the compressed matrix, plus the row-index entries the kernel
+        uses (64 bytes per block when it splits blocks over two half-waves)."""
+        split = _lib.nwc_token_split(self.n, self.in_features, self.code, int(self.row_index() is not None))
+        return self.bytes + (self.bases.numel() * LANES * 2 if split == 2 else 0)
+
     def linear_bf16(self, x: torch.Tensor, bias) -> torch.Tensor:
         """Token path: y = scale * (W x) + bias, x BF16 or fp32, y BF16."""
         _need_gpu(self.data)
@@ -269,8 +294,10 @@ class NWCWeight:
         sp = _ptr(self.scale) if self.scale is not None else None
         if x.dtype == torch.bfloat16 or self.layout:
             xin = self._x16(x if x.dtype == torch.bfloat16 else x.to(torch.bfloat16)).contiguous()
+            ri = self.row_index()
             err = _lib.nwc_linear_xbf16(_stream(), _ptr(self.data), _ptr(self.bases), _ptr(self.hdr), _ptr(self.lut),
-                                        _ptr(self.low), _ptr(xin), bp, sp, _ptr(y), self.n, self.in_features, self.code)
+                                        _ptr(self.low), _ptr(ri) if ri is not None else None, _ptr(xin), bp, sp, _ptr(y),
+                                        self.n, self.in_features, self.code)
         else:                                                      # layout 0 with fp32 activations: the reference ABI
             xin = self._x16(x.float()).contiguous()
             err = _lib.nwc_linear_bf16(_stream(), _ptr(self.data), _ptr(self.bases), _ptr(self.hdr), _ptr(self.lut),

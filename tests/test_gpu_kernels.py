@@ -141,3 +141,65 @@ def test_full_size_qwen3_4b_gate_up(cuda, layout):
     assert np.all(err <= 2.0 ** -8 * np.abs(y64) + 1e-5)
     y32 = c.matvec(x.float()).double().cpu().numpy()
     assert np.all(np.abs(y32 - y64) <= 1e-3 * np.abs(y64) + 1e-5)
+
+
+def _row_index_cpu(w, lut):
+    """Bit positions of rows 2, 4, 6 in every layout-0 lane stream, from the code lengths (rank r: r + 2 bits, rank
+    >= 15: 24-bit escape, fillers past M or K: rank 0; docs/format.md section 3) with exp_of_rank read back from the
+    table as the decoders do."""
+    M, K = w.shape
+    K16, CB = (K + 15) // 16 * 16, (K + 511) // 512
+    Mp = (M + 7) // 8 * 8
+    hb = np.zeros((Mp, CB * 512), np.int64)
+    hb[:M, :K] = (bits16(w).reshape(M, K).astype(np.int64) >> 8) & 0x7F
+    lut = lut.astype(np.uint32)
+    eor = []
+    for q in range(15):
+        src = (1 << (11 - q)) if q < 11 else (q - 11) >> 1
+        sh = 8 if (q < 11 or (q & 1)) else 16
+        eor.append(int((lut[src] >> sh) & 0x7F))
+    rank = np.full(128, 15)
+    for r in range(14, -1, -1):
+        rank[eor[r]] = r
+    ln = np.where(rank[hb] < 15, rank[hb] + 2, 24)
+    ln[M:, :] = 2                                                      # filler weights are coded as rank 0, sign 0
+    ln[:, K:] = 2
+    ln = ln.reshape(Mp // 8, 8, CB, 32, 16).sum(-1)                 # bits per (group, row, block column, lane)
+    cum = np.cumsum(ln, axis=1)                                        # after rows 0..r
+    pos = cum[:, [1, 3, 5], :, :]                                      # starts of rows 2, 4, 6
+    return pos.transpose(0, 2, 1, 3).reshape(-1, 3, 32), K16           # [block = group * CB + cb][j][lane]
+
+
+@pytest.mark.parametrize("M,K,escapes", [(64, 2048, False), (100, 1000, True), (13, 40, True), (300, 2560, False)])
+def test_row_index_values(cuda, M, K, escapes):
+    NWCWeight, _, _ = _nwc()
+    w = bf16_matrix(M, K, seed=M + K, escapes=escapes)
+    c = NWCWeight(w, device="cuda", layout=0)
+    got = c.row_index().cpu().numpy().view(np.uint16).reshape(-1, 3, 32).astype(np.int64)
+    want, K16 = _row_index_cpu(w, c.lut.cpu().numpy().view(np.uint32))
+    CB = (K + 511) // 512
+    lane_ok = (np.arange(CB)[:, None] * 512 + np.arange(32)[None, :] * 16) < K16        # lanes with columns
+    mask = np.broadcast_to(np.tile(lane_ok, ((M + 7) // 8, 1))[:, None, :], want.shape)
+    assert np.array_equal(got[mask], want[mask])
+
+
+def test_token_path_with_and_without_row_index(cuda):
+    """The split decode (two half-waves per block, reduce over 4 rows) against the whole-block decode."""
+    import ctypes
+    from nwc_amd.nwc_torch import _lib, _ptr, _stream
+    NWCWeight, _, _ = _nwc()
+    M, K = 2560, 4096                                                  # o_proj: small enough for the split plan
+    w = bf16_matrix(M, K, seed=77, escapes=False)
+    c = NWCWeight(w, device="cuda", layout=0)
+    assert _lib.nwc_token_split(c.n, K, c.code, 1) == 2
+    x = torch.randn(K, generator=torch.Generator().manual_seed(6)).to(torch.bfloat16).cuda()
+    ys = []
+    for ri in (c.row_index(), None):
+        y = torch.empty(M, dtype=torch.bfloat16, device="cuda")
+        err = _lib.nwc_linear_xbf16(_stream(), _ptr(c.data), _ptr(c.bases), _ptr(c.hdr), _ptr(c.lut), _ptr(c.low),
+                                    _ptr(ri) if ri is not None else None, _ptr(x), None, None, _ptr(y), c.n, K, c.code)
+        assert err == 0
+        ys.append(y.double().cpu().numpy())
+    y64 = (w.cuda().double() @ x.double()).cpu().numpy()
+    for y in ys:
+        assert np.all(np.abs(y - y64) <= 2.0 ** -8 * np.abs(y64) + 1e-5)
