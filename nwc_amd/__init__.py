@@ -12,8 +12,20 @@ is the drop-in.
 """
 __version__ = "0.10.1"
 
-from .nwc_torch import NWCWeight, NWCLinear, NWCEmbedding, convert, fuse, fits, choose_block, quantize_fp8  # noqa: E402
-from .checkpoint import save_pretrained, load_pretrained, export_bf16                                     # noqa: E402
-
 __all__ = ["NWCWeight", "NWCLinear", "NWCEmbedding", "convert", "fuse", "fits", "choose_block",
            "quantize_fp8", "save_pretrained", "load_pretrained", "export_bf16", "__version__"]
+
+_FROM = {**{n: "nwc_torch" for n in ("NWCWeight", "NWCLinear", "NWCEmbedding", "convert", "fuse", "fits", "choose_block",
+                                      "quantize_fp8")},
+         **{n: "checkpoint" for n in ("save_pretrained", "load_pretrained", "export_bf16")}}
+
+
+def __getattr__(name):
+    """The public names load the HIP library on first use (ImportError when it is not built), so that
+    `python -m nwc_amd.build` works before the library exists."""
+    if name in _FROM:
+        import importlib
+        value = getattr(importlib.import_module(f".{_FROM[name]}", __name__), name)
+        globals()[name] = value
+        return value
+    raise AttributeError(f"module {__name__!r} has no attribute {name!r}")
