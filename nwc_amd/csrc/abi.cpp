@@ -45,39 +45,56 @@ uint32_t slot_words_for(int layout) { return layout == 0 ? kSlotWords0 : layout 
 // latency hiding); larger tiles are spread evenly over at most 16 half-waves that each decode several blocks, one
 // round at a time, through two region buffers (PIPE = true).
 constexpr uint32_t kDynLdsPipe = 62u * 1024u;         // two such workgroups per CU next to their decode tables
+// A round buffer of 440 words per block holds the ~350-400 words of N(0, 0.02^2) or real-model BF16 blocks (a round
+// that does not fit decodes from global memory), so 32 blocks fit two workgroups per CU.
+constexpr uint32_t kSlotWords2 = 440;
 
 bool plan_layout0(const Shape &f, int mode, int ncu, bool index, LaunchPlan &p) {
     p = LaunchPlan{};
     p.layout = 0;
     const bool rows = mode == kToken || mode == kF32;
-    const uint32_t CB = f.CB, groups = f.groups(), slot = kSlotWords0;
+    const uint32_t CB = f.CB, groups = f.groups(), ncu_ = (uint32_t)ncu;
     const uint32_t part = rows ? kRows0 * CB * 4u : 0u;                // row-sum bytes per row group
-    uint32_t G = std::max(1u, (groups + 2u * (uint32_t)ncu - 1u) / (2u * (uint32_t)ncu));
+    auto ceil_div = [](uint32_t a, uint32_t b) { return (a + b - 1u) / b; };
+    auto set = [&](bool pipe, uint32_t split, uint32_t G, uint32_t halves, uint32_t slot, uint32_t lds) {
+        p.pipe = pipe;
+        p.split = split;
+        p.G = G;
+        p.threads = 32u * halves;
+        p.grid = ceil_div(groups, G);
+        p.slot_words = slot;
+        p.lds = lds;
+        return true;
+    };
+    // 1. small matrices with the row index: two half-waves per block (rows 0-3 / 4-7), two workgroups per CU
+    if (index && rows) {
+        const uint32_t G = std::max(1u, ceil_div(groups, 2u * ncu_)), blocks = G * CB;
+        const uint32_t lds = blocks * kSlotWords0 * 4u + G * part;
+        if (2u * blocks <= 20u && lds <= kDynLdsPipe) return set(false, 2u, G, 2u * blocks, kSlotWords0, lds);
+    }
+    // 2. one block per half-wave, one round: two workgroups of up to 32 half-waves (16 waves) per CU, which the
+    //    58-VGPR kernel allows (8 waves per SIMD)
+    {
+        const uint32_t G = std::max(1u, ceil_div(groups, 2u * ncu_)), blocks = G * CB;
+        const uint32_t halves = (blocks + 1u) & ~1u;
+        const uint32_t lds = halves * kSlotWords2 * 4u + G * part;
+        if (blocks <= 32u && lds <= kDynLdsPipe) return set(false, 1u, G, halves, kSlotWords2, lds);
+    }
+    // 3. several blocks per half-wave: rounds through two region buffers, two workgroups per CU
+    uint32_t G = std::max(1u, ceil_div(groups, 2u * ncu_));
     for (;; G--) {
         const uint32_t blocks = G * CB;
-        uint32_t halves, lds, split = 1;
-        bool pipe;
+        uint32_t halves, lds;
         if (blocks <= 20) {
-            // with the row index, two half-waves share a block (rows 0-3 / 4-7) while the tile stays <= 20 half-waves
-            split = index && rows && 2u * blocks <= 20u ? 2u : 1u;
-            halves = split == 2u ? 2u * blocks : (blocks + 1u) & ~1u;
-            lds = (halves / split) * slot * 4u + G * part;
-            pipe = false;
+            halves = (blocks + 1u) & ~1u;
+            lds = halves * kSlotWords0 * 4u + G * part;
+            if (lds <= kDynLdsPipe) return set(false, 1u, G, halves, kSlotWords0, lds);
         } else {
             const uint32_t rounds = (blocks + 15u) / 16u;
             halves = ((blocks + rounds - 1u) / rounds + 1u) & ~1u;
-            while (halves > 2 && halves * 2u * slot * 4u + G * part > kDynLdsPipe) halves -= 2;
-            lds = halves * 2u * slot * 4u + G * part;
-            pipe = true;
-        }
-        if (lds <= kDynLdsPipe) {
-            p.pipe = pipe;
-            p.split = split;
-            p.G = G;
-            p.threads = 32u * halves;
-            p.grid = (groups + G - 1u) / G;
-            p.lds = lds;
-            return true;
+            while (halves > 2 && halves * 2u * kSlotWords0 * 4u + G * part > kDynLdsPipe) halves -= 2;
+            lds = halves * 2u * kSlotWords0 * 4u + G * part;
+            if (lds <= kDynLdsPipe) return set(true, 1u, G, halves, kSlotWords0, lds);
         }
         if (G == 1) return false;                            // K beyond ~190k columns
     }
@@ -122,7 +139,8 @@ int run_blocks(int mode, bool xbf16, hipStream_t st, const uint8_t *data, const 
     const Shape f((uint32_t)(n / K), K, layout);
     LaunchPlan p;
     if (!plan_blocks(f, layout, mode, ncu, aux != nullptr && layout == 0, p)) return -1;
-    BlockArgs a{data, bases, hdr, tab, low, x, bias, scale, out, aux, f.M, f.K, p.G, slot_words_for(layout)};
+    BlockArgs a{data, bases, hdr, tab, low, x, bias, scale, out, aux, f.M, f.K, p.G,
+                layout == 0 ? p.slot_words : slot_words_for(layout)};
     return layout == 2 ? launch_fixed(p, t, mode, xbf16, a, st) : launch_prefix(p, t, mode, xbf16, a, st);
 }
 

@@ -187,12 +187,12 @@ __device__ __forceinline__ float row0(Seq<ELEM> &S, const LutLds &s, const uint4
 }
 
 // Rows r0 .. r0 + NR - 1 of one layout-0 block for one lane, decoded from LDS starting at bit position P0 of the lane's
-// stream, with those raw-plane rows already requested.  Returns the row sums reduced over the half-wave (NR = 8: lane
+// stream, with the first four of those raw-plane rows already requested into `ring`.  Returns the row sums reduced over the half-wave (NR = 8: lane
 // 4r holds row r0 + r; NR = 4: lane 8r) or, for dequantization, stores the rows; MODE kRowIndex records the row
 // index (positions of rows 2, 4, 6) instead.  Fully unrolled: every row's raw bytes live in their own registers.
 template <int ELEM, int MODE, bool XBF16, int NR>
 __device__ __forceinline__ float rowsN(const LutLds &s, const uint32_t *lane, uint32_t P0, const BlockArgs &a, const Shape &f,
-                                       const XRegs<XBF16> &x, const uint4 raw[NR], const Coord0 &c, uint32_t r0, uint32_t L) {
+                                       const XRegs<XBF16> &x, uint4 ring[4], const Coord0 &c, uint32_t r0, uint32_t L) {
     Seq<ELEM> S;
     S.init_at(lane, P0);
     float acc[NR];
@@ -201,7 +201,9 @@ __device__ __forceinline__ float rowsN(const LutLds &s, const uint32_t *lane, ui
         if (MODE == kRowIndex && r > 0 && (r & 1) == 0)
             ((uint16_t *)a.out)[((uint64_t)c.b * kRowIndexSplits + (r >> 1) - 1) * kLanes + L] = (uint16_t)S.position(lane);
         uint32_t pw[8];
-        const float sum = row0<ELEM, MODE, XBF16>(S, s, raw[r], x, pw);
+        const float sum = row0<ELEM, MODE, XBF16>(S, s, ring[r & 3], x, pw);
+        // eight rows go through a ring of four registers: row r + 4 is requested when row r is done
+        if (MODE != kRowIndex && r + 4 < NR) ring[r & 3] = raw_row<ELEM>(a.low, f, c, r0 + r + 4);
         if (MODE == kDequant) store_row0<MODE>(a, f, c.row0 + r0 + r, c.col0, c.col_ok, pw);
         else acc[r] = c.col_ok ? sum : 0.f;
     }
@@ -339,9 +341,9 @@ __global__ void __launch_bounds__(1024) k_layout0(BlockArgs a) {
     if constexpr (!PIPE) {
         // the table is stored before the raw rows are requested, so its registers are free for them
         lut_commit<kLutSeq>(s, Q, a.lut);
-        uint4 raw[NR];
+        uint4 raw[4];
 #pragma unroll
-        for (int r = 0; r < NR; r++) raw[r] = MODE == kRowIndex ? make_uint4(0u, 0u, 0u, 0u) : raw_row<ELEM>(a.low, f, c, r0 + r);
+        for (int r = 0; r < 4; r++) raw[r] = MODE == kRowIndex ? make_uint4(0u, 0u, 0u, 0u) : raw_row<ELEM>(a.low, f, c, r0 + r);
         const bool fits = R.n16 * 4u <= cap;
         if (fits) bulk_commit(Bk, cur, R, tid, nth);
         __syncthreads();

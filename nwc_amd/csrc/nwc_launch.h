@@ -9,6 +9,7 @@ struct LaunchPlan {
     bool pipe;              // layout 0: rounds through two region buffers, the next round prefetched
     uint32_t split;         // layout 0: half-waves per block (1, or 2 with the row index)
     uint32_t grid, threads, lds, G;
+    uint32_t slot_words;    // layout 0: region-buffer words per block
 };
 
 int launch_prefix(const LaunchPlan &p, int elem_t, int mode, bool xbf16, const BlockArgs &a, hipStream_t st);
