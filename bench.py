@@ -2,17 +2,27 @@
 """Benchmark of the batch-1 fused decode-matvec on one MI355X (BASELINE.json metric: per-token matvec us + effective
 HBM GB/s, Qwen3-4B shapes, batch 1, vs a BF16 hipBLASLt matvec).
 
-Workload: a Qwen3-4B-shaped stack of 36 layers, each with the fused qkv 6144x2560,
+Default workload: a Qwen3-4B-shaped stack of 36 layers, each with the fused qkv 6144x2560,
 o_proj 2560x4096, fused gate_up 19456x2560 and down 2560x9728 matrices, BF16, layout 0 (--layout 1 for the other
 layout of that config).  One step = one token: the 144 token-path matvecs of the stack, captured once as a HIP graph
 and replayed.  Weights are N(0, 0.02^2) from fixed seeds; each of the four matrices is encoded once and copied to
 36 distinct device buffers (the sweep reads 36 x 4 different buffers, far beyond the 256 MB Infinity Cache).
 
-Reported: value = algorithmic bytes per token / GPU time per token (GB/s), with the per-launch medians (HIP events),
-the same sweep with hipBLASLt BF16 matvecs (F.linear), the roofline of the dominant kernel (the gate_up launch:
-algorithmic bytes / average launch time; HBM traffic from the committed counter summary profiles/traffic_gate_up.json)
-and the CPU baseline (the C oracle's decode + fp32 matvec of configs[0], on the host cores).
-usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--layout 0] [--cpu-seconds 10]
+Reported: value = algorithmic bytes per token / GPU time per token (GB/s), with per-launch times (a HIP graph of the
+36 copies' launches of one shape, and single launches between HIP events as the reference's kernbench does), the same
+sweep with hipBLASLt BF16 matvecs (F.linear), the roofline of the dominant kernel (the gate_up launch: algorithmic
+bytes / average launch time; HBM traffic from the committed counter summary profiles/traffic_gate_up.json) and the
+CPU baseline (the C oracle's decode + fp32 matvec of configs[0], on the host cores).
+
+The other BASELINE configs, each printed as one JSON line of its own (not the driver's line):
+  --config qwen3-0.6b      configs[1]: 28 layers of 4096x1024 / 1024x2048 / 6144x1024 / 1024x3072, BF16 layout 0
+  --config qwen3-4b-fp8    configs[3]: the 4B stack as weight-only fp8 e4m3 (per-row scale), layout 0 or 1, against
+                           the library's uncompressed fp8 matvec (nwc_ref_fp8) and hipBLASLt BF16
+  --config qwen2.5-7b-l2   configs[4]: 28 layers of 4608x3584 / 3584x3584 / 37888x3584 / 3584x18944, BF16 layout 2
+  --prefill 512            configs[2] prefill: per matrix, dequantization to a BF16 buffer + hipBLASLt GEMM of 512
+                           tokens, against the GEMM on resident BF16 weights
+  --gather 64              configs[4] embedding: 64 seeded ids from the 152064x3584 table, layouts 0, 1 and 2
+usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--layout 0] [--cpu-seconds 10] [--config NAME]
        python bench.py --profile-launches 20     (counter target for rocprofv3 --pmc: copies + gate_up launches)
 """
 import argparse
@@ -30,6 +40,16 @@ METRIC = "per-token matvec µs + effective HBM GB/s, Qwen3-4B shapes batch 1 vs 
 PEAK_HBM_GBS = 8000.0
 LAYERS = 36
 SHAPES = [("qkv", 6144, 2560), ("o", 2560, 4096), ("gate_up", 19456, 2560), ("down", 2560, 9728)]
+# BASELINE configs by name: (layers, shapes, element type, default layout, workload text)
+CONFIGS = {
+    "qwen3-4b": (36, SHAPES, "bf16", 0, "Qwen3-4B-shaped 36-layer batch-1 token sweep (BASELINE configs[2])"),
+    "qwen3-0.6b": (28, [("qkv", 4096, 1024), ("o", 1024, 2048), ("gate_up", 6144, 1024), ("down", 1024, 3072)], "bf16", 0,
+                   "Qwen3-0.6B-shaped 28-layer batch-1 token sweep (BASELINE configs[1])"),
+    "qwen3-4b-fp8": (36, SHAPES, "fp8", 0, "Qwen3-4B-shaped 36-layer batch-1 token sweep, weight-only fp8 e4m3 with "
+                                           "per-row scale (BASELINE configs[3])"),
+    "qwen2.5-7b-l2": (28, [("qkv", 4608, 3584), ("o", 3584, 3584), ("gate_up", 37888, 3584), ("down", 3584, 18944)],
+                      "bf16", 2, "Qwen2.5-7B-shaped 28-layer batch-1 token sweep, layout 2 (BASELINE configs[4])"),
+}
 
 
 def log(*a):
@@ -109,137 +129,227 @@ DOMINANT = "gate_up"            # the roofline's kernel: the largest matrix, k_l
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_gate_up.json")
 
 
-def run_gpu(args):
+def graph_stack(fns):
+    """Capture fns (one callable per launch) as one HIP graph; None if capture is refused."""
     import torch
-    from nwc_amd.nwc_torch import NWCWeight
-    torch.backends.cuda.preferred_blas_library("hipblaslt")
-    dev = torch.device("cuda:0")
-    props = torch.cuda.get_device_properties(dev)
-    log(f"device: {props.name} ({props.gcnArchName}), {props.multi_processor_count} CUs, {props.total_memory/2**30:.0f} GiB")
-    stream = torch.cuda.current_stream()
-
-    # ---- compressed stack ----
-    t0 = time.time()
-    base = []
-    for si, (name, M, K) in enumerate(SHAPES):
-        w = make_weight(M, K, 1000 + si)
-        c = NWCWeight(w, device=dev, layout=args.layout)
-        x = torch.randn(K, generator=torch.Generator().manual_seed(2000 + si)).to(torch.bfloat16).to(dev)
-        base.append((name, M, K, c, x, w))
-    copies = {name: [c] + [clone_weight(c) for _ in range(LAYERS - 1)] for name, M, K, c, x, w in base}
-    ys = {name: [torch.empty(M, dtype=torch.bfloat16, device=dev) for _ in range(LAYERS)] for name, M, K, *_ in base}
-    launches = {name: [Launch(copies[name][l], x, ys[name][l]) for l in range(LAYERS)] for name, M, K, c, x, w in base}
+    for f in fns:
+        f()
     torch.cuda.synchronize()
-    log(f"encoded + placed {len(SHAPES)}x{LAYERS} compressed matrices in {time.time()-t0:.1f} s")
-
-    # correctness spot check of the copies against a torch fp32 matvec
-    for name, M, K, c, x, w in base:
-        y = copies[name][LAYERS - 1].linear_bf16(x, None).float()
-        ref = (w.to(dev).float() @ x.float())
-        err = ((y - ref).abs() - (2 ** -8) * ref.abs()).max().item()
-        if err > 1e-5:
-            raise SystemExit(f"{name}: token path outside tolerance ({err:.3e})")
-
-    sh = ctypes.c_void_p(stream.cuda_stream)
-    bytes_tok = sum(c.token_bytes() + 2 * K + 2 * M for name, M, K, c, x, w in base) * LAYERS
-    bf16_tok = sum(2 * M * K + 2 * K + 2 * M for name, M, K, *_ in base) * LAYERS
-
-    # ---- per-launch medians (the reference kernbench's method) ----
-    per = []
-    for name, M, K, c, x, w in base:
-        L = launches[name]
-        for i in range(10):
-            L[i % LAYERS](sh)
-        ms, _ = event_ms(lambda j: L[j](sh), args.runs, LAYERS)
-        per.append({"layer": name, "M": M, "K": K, "nwc_bytes": c.token_bytes(), "nwc_us": ms * 1e3,
-                    "nwc_GBps": (c.token_bytes() + 2 * K + 2 * M) / (ms * 1e-3) / 1e9})
-
-    # ---- the timed sweep: one token = 144 launches, captured as a HIP graph ----
-    def sweep():
-        for l in range(LAYERS):
-            for name, *_ in base:
-                launches[name][l](ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
-
-    graph = None
     try:
-        sweep()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for f in fns:
+                f()
         torch.cuda.synchronize()
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph):
-            sweep()
-        torch.cuda.synchronize()
-    except Exception as e:  # capture refused: time the eager sweep instead
-        log(f"graph capture failed ({e}); timing the eager sweep")
-        graph = None
-    step = graph.replay if graph is not None else sweep
-    for _ in range(args.warmup):
+        return g
+    except Exception as e:
+        log(f"graph capture failed ({e}); timing eagerly")
+        return None
+
+
+def timed_steps(step, steps, warmup):
+    """GPU ms per step between two HIP events on the current stream."""
+    import torch
+    for _ in range(warmup):
         step()
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
-    for _ in range(args.steps):
+    for _ in range(steps):
         step()
     e1.record()
     torch.cuda.synchronize()
-    ms_step = e0.elapsed_time(e1) / args.steps
+    return e0.elapsed_time(e1) / steps
+
+
+def run_gpu(args, cfg):
+    import torch
+    from nwc_amd.nwc_torch import NWCWeight, quantize_fp8, ref_fp8_matvec
+    layers, shapes, elem, layout = cfg
+    torch.backends.cuda.preferred_blas_library("hipblaslt")
+    dev = torch.device("cuda:0")
+    props = torch.cuda.get_device_properties(dev)
+    log(f"device: {props.name} ({props.gcnArchName}), {props.multi_processor_count} CUs, {props.total_memory/2**30:.0f} GiB")
+    cur = lambda: ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+    # ---- compressed stack ----
+    t0 = time.time()
+    base = []
+    for si, (name, M, K) in enumerate(shapes):
+        w = make_weight(M, K, 1000 + si)
+        c = NWCWeight(w, device=dev, layout=layout, elem=elem)
+        x = torch.randn(K, generator=torch.Generator().manual_seed(2000 + si)).to(torch.bfloat16).to(dev)
+        base.append((name, M, K, c, x, w))
+    copies = {name: [c] + [clone_weight(c) for _ in range(layers - 1)] for name, M, K, c, x, w in base}
+    ys = {name: [torch.empty(M, dtype=torch.bfloat16, device=dev) for _ in range(layers)] for name, M, K, *_ in base}
+    launches = {name: [Launch(copies[name][l], x, ys[name][l]) for l in range(layers)] for name, M, K, c, x, w in base}
+    torch.cuda.synchronize()
+    log(f"encoded + placed {len(shapes)}x{layers} compressed matrices in {time.time()-t0:.1f} s")
+
+    # correctness spot check of the last copies against a torch fp32 matvec on the decoded weights
+    for name, M, K, c, x, w in base:
+        y = copies[name][layers - 1].linear_bf16(x, None).float()
+        wd = c.dequant().float()[:, :K]
+        if c.scale is not None:
+            wd = wd * c.scale[:, None]
+        ref = wd @ x.float()
+        err = ((y - ref).abs() - (2 ** -8) * ref.abs()).max().item()
+        if err > 1e-5:
+            raise SystemExit(f"{name}: token path outside tolerance ({err:.3e})")
+
+    bytes_tok = sum(c.token_bytes() + 2 * K + 2 * M for name, M, K, c, x, w in base) * layers
+    bf16_tok = sum(2 * M * K + 2 * K + 2 * M for name, M, K, *_ in base) * layers
+
+    # ---- per-launch times: a graph of the `layers` copies of one shape (kernel time) and single launches between
+    #      events (the reference kernbench's method, which includes the host's launch overhead for small kernels) ----
+    per = []
+    for name, M, K, c, x, w in base:
+        L = launches[name]
+        g = graph_stack([(lambda j=j: L[j](cur())) for j in range(layers)])
+        us = timed_steps(g.replay, 4, 1) / layers * 1e3 if g is not None else None
+        ev, _ = event_ms(lambda j: L[j](cur()), args.runs, layers)
+        nb = c.token_bytes() + 2 * K + 2 * M
+        per.append({"layer": name, "M": M, "K": K, "nwc_bytes": c.token_bytes(), "nwc_us": us, "nwc_us_event": ev * 1e3,
+                    "nwc_GBps": nb / (us * 1e-6) / 1e9 if us else None})
+        del g
+
+    # ---- the timed sweep: one token = all launches of the stack, captured as one HIP graph ----
+    def sweep():
+        for l in range(layers):
+            for name, *_ in base:
+                launches[name][l](cur())
+    graph = graph_stack([sweep])
+    ms_step = timed_steps(graph.replay if graph is not None else sweep, args.steps, args.warmup)
 
     # ---- hipBLASLt BF16 baseline: the same stack uncompressed ----
-    blas = None
+    blas = fp8 = None
     if not args.no_baseline:
         import torch.nn.functional as F
-        wcopy = {name: [w.to(dev) for _ in range(LAYERS)] for name, M, K, c, x, w in base}
+        wcopy = {name: [w.to(dev) for _ in range(layers)] for name, M, K, c, x, w in base}
         xs = {name: x.view(1, K) for name, M, K, c, x, w in base}
         blas_per = []
         for name, M, K, *_ in base:
             W = wcopy[name]
-            for i in range(10):
-                F.linear(xs[name], W[i % LAYERS])
-            ms, _ = event_ms(lambda j: F.linear(xs[name], W[j]), args.runs, LAYERS)
-            blas_per.append({"layer": name, "us": ms * 1e3, "GBps": (2 * M * K + 2 * K + 2 * M) / (ms * 1e-3) / 1e9})
+            g = graph_stack([(lambda j=j: F.linear(xs[name], W[j])) for j in range(layers)])
+            us = timed_steps(g.replay, 4, 1) / layers * 1e3 if g is not None else None
+            ev, _ = event_ms(lambda j: F.linear(xs[name], W[j]), args.runs, layers)
+            blas_per.append({"layer": name, "us": us, "us_event": ev * 1e3,
+                             "GBps": (2 * M * K + 2 * K + 2 * M) / (us * 1e-6) / 1e9 if us else None})
+            del g
 
         def bsweep():
-            for l in range(LAYERS):
+            for l in range(layers):
                 for name, *_ in base:
                     F.linear(xs[name], wcopy[name][l])
-        bgraph = None
-        try:
-            bsweep()
-            torch.cuda.synchronize()
-            bgraph = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(bgraph):
-                bsweep()
-            torch.cuda.synchronize()
-        except Exception as e:
-            log(f"hipBLASLt graph capture failed ({e}); eager sweep")
-            bgraph = None
-        bstep = bgraph.replay if bgraph is not None else bsweep
-        for _ in range(args.warmup):
-            bstep()
-        torch.cuda.synchronize()
-        e0.record()
-        for _ in range(args.steps):
-            bstep()
-        e1.record()
-        torch.cuda.synchronize()
-        bms = e0.elapsed_time(e1) / args.steps
-        blas = {"us_per_token_graph": bms * 1e3, "us_per_token_sum_of_launches": LAYERS * sum(p["us"] for p in blas_per),
+        bgraph = graph_stack([bsweep])
+        bms = timed_steps(bgraph.replay if bgraph is not None else bsweep, args.steps, args.warmup)
+        blas = {"us_per_token_graph": bms * 1e3, "us_per_token_sum_of_launches": layers * sum(p["us"] for p in blas_per),
                 "GBps": bf16_tok / (bms * 1e-3) / 1e9, "per_layer": blas_per, "bytes_per_token": bf16_tok,
                 "library": "torch F.linear, preferred_blas_library=hipblaslt"}
-        del wcopy
+        del wcopy, bgraph
         torch.cuda.empty_cache()
+        if elem == "fp8":
+            # the library's uncompressed fp8 weight-only matvec on the same quantized weights (1 byte per weight)
+            q8 = {}
+            for name, M, K, c, x, w in base:
+                q, sc = quantize_fp8(w)
+                q8[name] = ([q.to(dev) for _ in range(layers)], sc.to(dev), x.float().to(dev))
+            fp8_tok = sum(M * K + 4 * M + 4 * K + 2 * M for name, M, K, *_ in base) * layers
+
+            def fsweep():
+                for l in range(layers):
+                    for name, *_ in base:
+                        qs, sc, xf = q8[name]
+                        ref_fp8_matvec(qs[l], sc, xf)
+            fgraph = graph_stack([fsweep])
+            fms = timed_steps(fgraph.replay if fgraph is not None else fsweep, args.steps, args.warmup)
+            fp8 = {"us_per_token_graph": fms * 1e3, "GBps": fp8_tok / (fms * 1e-3) / 1e9, "bytes_per_token": fp8_tok,
+                   "library": "nwc_ref_fp8 (uncompressed fp8 e4m3 + fp32 row scale, 1 byte per weight)"}
+            del q8, fgraph
+            torch.cuda.empty_cache()
 
     # ---- roofline of the dominant kernel: average launch time of back-to-back gate_up launches ----
     name, M, K, c, x, w = next(b for b in base if b[0] == DOMINANT)
     L = launches[name]
     dom_bytes = c.token_bytes() + 2 * K + 2 * M
-    dom_ms = avg_launch_ms(lambda j: L[j](ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)), LAYERS, 4)
-    sum_launch_us = LAYERS * sum(p["nwc_us"] for p in per)
+    dom_ms = avg_launch_ms(lambda j: L[j](cur()), layers, 4)
+    sum_launch_us = layers * sum(p["nwc_us"] for p in per)
     return {
         "ms_step": ms_step, "graph": graph is not None, "bytes_tok": bytes_tok, "bf16_tok": bf16_tok, "per": per,
         "sum_launch_us": sum_launch_us, "dom_bytes": dom_bytes, "dom_us": dom_ms * 1e3,
-        "achieved": dom_bytes / (dom_ms * 1e-3) / 1e9, "blas": blas,
+        "achieved": dom_bytes / (dom_ms * 1e-3) / 1e9, "blas": blas, "fp8": fp8,
         "device": {"name": props.name, "arch": props.gcnArchName, "cus": props.multi_processor_count},
     }
+
+
+def run_prefill(args):
+    """configs[2] prefill: per 4B matrix, dequantization into a BF16 buffer + the hipBLASLt GEMM of --prefill tokens,
+    against the same GEMM on resident BF16 weights; 8 copies rotate so every launch reads HBM."""
+    import torch
+    import torch.nn.functional as F
+    from nwc_amd.nwc_torch import NWCWeight
+    torch.backends.cuda.preferred_blas_library("hipblaslt")
+    dev = torch.device("cuda:0")
+    T, R = args.prefill, 8
+    rows = []
+    for si, (name, M, K) in enumerate(SHAPES):
+        w = make_weight(M, K, 1000 + si)
+        c = NWCWeight(w, device=dev, layout=args.layout)
+        cs = [c] + [clone_weight(c) for _ in range(R - 1)]
+        wb = [w.to(dev) for _ in range(R)]
+        tmp = torch.empty(M, c.K16, dtype=torch.bfloat16, device=dev)
+        x = torch.randn(T, K, generator=torch.Generator().manual_seed(3000 + si)).to(torch.bfloat16).to(dev)
+        y = F.linear(x, cs[R - 1].dequant(tmp)[:, :K])
+        ref = F.linear(x, wb[0])
+        if not torch.equal(y, ref):                 # same BF16 weights, same GEMM: identical outputs
+            raise SystemExit(f"{name}: prefill through the compressed weights differs from the resident GEMM")
+        t = {}
+        for key, fns in (("dequant", [(lambda j=j: cs[j].dequant(tmp)) for j in range(R)]),
+                         ("gemm", [(lambda j=j: F.linear(x, tmp[:, :K])) for j in range(R)]),
+                         ("dequant_gemm", [(lambda j=j: F.linear(x, cs[j].dequant(tmp)[:, :K])) for j in range(R)]),
+                         ("resident_bf16", [(lambda j=j: F.linear(x, wb[j])) for j in range(R)])):
+            g = graph_stack(fns)
+            t[key] = timed_steps(g.replay if g is not None else (lambda: [f() for f in fns]), 5, 2) / R * 1e3
+            del g
+        dq_bytes = c.bytes + 2 * M * c.K16
+        rows.append({"layer": name, "M": M, "K": K, "tokens": T, **{k + "_us": round(v, 2) for k, v in t.items()},
+                     "dequant_GBps": round(dq_bytes / (t["dequant"] * 1e-6) / 1e9, 1),
+                     "gemm_TFLOPs": round(2 * T * M * K / (t["gemm"] * 1e-6) / 1e12, 1)})
+        del cs, wb, tmp
+        torch.cuda.empty_cache()
+    tot = {k: round(LAYERS * sum(r[k] for r in rows), 1) for k in ("dequant_us", "gemm_us", "dequant_gemm_us", "resident_bf16_us")}
+    return {"metric": f"{args.prefill}-token prefill per Qwen3-4B stack: dequant to BF16 + hipBLASLt GEMM vs resident BF16 GEMM",
+            "value": tot["dequant_gemm_us"], "unit": "us", "higher_is_better": False, "dtype": "bf16",
+            "config": {"workload": "Qwen3-4B-shaped prefill (BASELINE configs[2]), 36 layers", "layout": args.layout,
+                       "tokens": T},
+            "per_stack": tot, "overhead_vs_resident": round(tot["dequant_gemm_us"] / tot["resident_bf16_us"], 3),
+            "per_layer": rows, "data": "synthetic N(0,0.02^2) BF16 weights, N(0,1) activations"}
+
+
+def run_gather(args):
+    """configs[4] embedding: --gather seeded uniform ids from the 152064 x 3584 table, per layout; 16 id sets rotate."""
+    import torch
+    from nwc_amd.nwc_torch import NWCWeight
+    dev = torch.device("cuda:0")
+    M, K, n = 152064, 3584, args.gather
+    w = make_weight(M, K, 4000)
+    out = {}
+    for layout in (0, 1, 2):
+        c = NWCWeight(w, device=dev, layout=layout)
+        ids = [torch.randint(0, M, (n,), generator=torch.Generator().manual_seed(5000 + i)).to(dev) for i in range(16)]
+        got = c.gather(ids[0])
+        if not torch.equal(got.cpu(), w[ids[0].cpu()]):
+            raise SystemExit(f"layout {layout}: gather is not bit-exact")
+        g = graph_stack([(lambda j=j: c.gather(ids[j])) for j in range(16)])
+        us = timed_steps(g.replay if g is not None else (lambda: [c.gather(i) for i in ids]), 5, 2) / 16 * 1e3
+        out[f"layout{layout}"] = {"us": round(us, 2), "table_MB": round(c.bytes / 1e6, 1),
+                                  "out_KB": round(n * K * 2 / 1e3, 1)}
+        del c, g
+        torch.cuda.empty_cache()
+    return {"metric": f"embedding gather of {n} ids from a 152064x3584 compressed table, us per call",
+            "value": out["layout2"]["us"], "unit": "us", "higher_is_better": False, "dtype": "bf16",
+            "config": {"workload": "Qwen2.5-7B untied embedding (BASELINE configs[4])", "ids": n},
+            "per_layout": out, "data": "synthetic N(0,0.02^2) BF16 table, uniform ids from fixed seeds"}
 
 
 def run_cpu(args):
@@ -318,6 +428,9 @@ def main():
     ap.add_argument("--no-baseline", action="store_true")
     ap.add_argument("--profile-launches", type=int, default=0,
                     help="only run the counter target (copies + this many gate_up launches), for rocprofv3 --pmc")
+    ap.add_argument("--config", default="qwen3-4b", choices=sorted(CONFIGS))
+    ap.add_argument("--prefill", type=int, default=0, help="time the prefill path for this many tokens instead")
+    ap.add_argument("--gather", type=int, default=0, help="time the embedding gather of this many ids instead")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -327,36 +440,46 @@ def main():
     if args.profile_launches:
         run_profile(args)
         return
+    if args.prefill or args.gather:
+        print(json.dumps(run_prefill(args) if args.prefill else run_gather(args)), flush=True)
+        return
 
-    g = run_gpu(args)
-    cpu = None if args.no_cpu else run_cpu(args)
+    layers, shapes, elem, layout0, workload = CONFIGS[args.config]
+    layout = args.layout if args.config in ("qwen3-4b", "qwen3-4b-fp8") else layout0
+    g = run_gpu(args, (layers, shapes, elem, layout))
+    cpu = None if args.no_cpu or args.config != "qwen3-4b" else run_cpu(args)
     us_tok = g["ms_step"] * 1e3
     value = g["bytes_tok"] / (g["ms_step"] * 1e-3) / 1e9
     blas = g["blas"]
+    rnd = lambda d: {k: (round(v, 2) if isinstance(v, float) else v) for k, v in d.items()}
     line = {
-        "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "metric": METRIC if args.config == "qwen3-4b" else f"per-token matvec µs + effective HBM GB/s, {args.config} "
+                  "shapes batch 1", "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(g["ms_step"], 4), "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "bf16",
-        "data": "synthetic: N(0,0.02^2) BF16 weights and N(0,1) activations from fixed seeds; 4 matrices encoded once, "
-                "36 device copies each",
-        "config": {"workload": f"Qwen3-4B-shaped 36-layer batch-1 token sweep (BASELINE configs[2]), layout {args.layout} BF16",
-                   "layers": LAYERS, "shapes": {n: [M, K] for n, M, K in SHAPES}, "layout": args.layout, "batch": 1,
-                   "step": "one token = 144 fused decode-matvecs replayed as one HIP graph" if g["graph"] else
-                           "one token = 144 fused decode-matvecs (eager)"},
+        "vs_baseline": None, "dtype": "fp8" if elem == "fp8" else "bf16",
+        "data": f"synthetic: N(0,0.02^2) {'weights quantized to fp8 e4m3 per row' if elem == 'fp8' else 'BF16 weights'} "
+                f"and N(0,1) activations from fixed seeds; {len(shapes)} matrices encoded once, {layers} device copies each",
+        "config": {"workload": f"{workload}, layout {layout}", "layers": layers,
+                   "shapes": {n: [M, K] for n, M, K in shapes}, "layout": layout, "elem": elem, "batch": 1,
+                   "step": f"one token = {layers * len(shapes)} fused decode-matvecs replayed as one HIP graph"
+                           if g["graph"] else f"one token = {layers * len(shapes)} fused decode-matvecs (eager)"},
         "us_per_token": round(us_tok, 1),
         "us_per_token_sum_of_launches": round(g["sum_launch_us"], 1),
         "bytes_per_token": g["bytes_tok"], "bytes_per_token_bf16": g["bf16_tok"],
         "hbm_frac": round(value / PEAK_HBM_GBS, 4),
-        "per_layer": [{k: (round(v, 2) if isinstance(v, float) else v) for k, v in p.items()} for p in g["per"]],
-        "hipblaslt": None if blas is None else {k: (round(v, 2) if isinstance(v, float) else v) for k, v in blas.items()},
+        "per_layer": [rnd(p) for p in g["per"]],
+        "hipblaslt": None if blas is None else rnd({**blas, "per_layer": [rnd(p) for p in blas["per_layer"]]}),
         "speedup_vs_hipblaslt": None if blas is None else round(blas["us_per_token_graph"] / us_tok, 3),
+        "native_fp8": None if g["fp8"] is None else rnd(g["fp8"]),
+        "speedup_vs_native_fp8": None if g["fp8"] is None else round(g["fp8"]["us_per_token_graph"] / us_tok, 3),
         "roofline": {"bound": "hbm", "achieved": round(g["achieved"], 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": round(g["achieved"] / PEAK_HBM_GBS, 4), "traffic": traffic_bytes(),
-                     "kernel": "k_layout0<0, 0, true, true> (BF16, token, BF16 x, pipelined): gate_up 19456x2560",
+                     "frac": round(g["achieved"] / PEAK_HBM_GBS, 4), "traffic": traffic_bytes() if args.config == "qwen3-4b" and layout == 0 else None,
+                     "kernel": f"{'k_layout0<BF16, token, BF16 x, single round, 8 rows>' if layout == 0 else f'layout {layout} kernel'}"
+                               f": gate_up {dict((n, (M, K)) for n, M, K in shapes)['gate_up']}",
                      "bytes_per_launch": g["dom_bytes"], "avg_launch_us": round(g["dom_us"], 2),
-                     "achieved_basis": "NWCWeight.bytes + x + y of one gate_up launch / average time of "
-                                       f"{4 * LAYERS} launches (a HIP graph of {LAYERS} back-to-back launches replayed 4 "
-                                       "times between HIP events on the launch stream)",
+                     "achieved_basis": "NWCWeight.bytes (+ row-index entries read) + x + y of one gate_up launch / "
+                                       f"average time of {4 * layers} launches (a HIP graph of {layers} back-to-back "
+                                       "launches replayed 4 times between HIP events on the launch stream)",
                      "sweep_achieved": round(g["bytes_tok"] / (g["sum_launch_us"] * 1e-6) / 1e9, 1)},
         "cpu_baseline": cpu,
         "device": g["device"],

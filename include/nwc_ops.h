@@ -62,7 +62,7 @@ int nwc_linear_bf16(void *stream, const uint8_t *data, const uint32_t *bases, co
 
 /* Token path with x as BF16 for every layout (layout 0: BF16 [K16]; layouts 1/2: BF16 [K32]), otherwise as
  * nwc_linear_bf16.  row_index: the layout-0 row index from nwc_row_index, or NULL; with it, small matrices decode
- * each block's rows 0-3 and 4-7 on two half-waves at once (same results).  No counterpart in the reference, whose
+ * each block's rows on two half-waves (rows 0-3, 4-7) or four (rows 0-1, 2-3, 4-5, 6-7) at once (same results).  No counterpart in the reference, whose
  * Python side converts x to fp32 for layout 0 with an extra kernel (nwc_torch.py:238-239); callers that hold BF16
  * activations use this one. */
 int nwc_linear_xbf16(void *stream, const uint8_t *data, const uint32_t *bases, const uint8_t *hdr, const uint32_t *tab,
@@ -76,7 +76,7 @@ int nwc_linear_xbf16(void *stream, const uint8_t *data, const uint32_t *bases, c
 int nwc_row_index(void *stream, const uint8_t *data, const uint32_t *bases, const uint8_t *hdr, const uint32_t *tab,
                   const uint8_t *low, uint16_t *row_index, uint64_t n, uint32_t K, int elem);
 
-/* Half-waves per block that nwc_linear_xbf16 would use on the current device (1, or 2 with a row index), for byte
+/* Half-waves per block that nwc_linear_xbf16 would use on the current device (1, or 2 or 4 with a row index), for byte
  * accounting; -1 for a bad shape.  No counterpart in the reference. */
 int nwc_token_split(uint64_t n, uint32_t K, int elem, int with_row_index);
 

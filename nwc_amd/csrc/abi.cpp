@@ -66,11 +66,15 @@ bool plan_layout0(const Shape &f, int mode, int ncu, bool index, LaunchPlan &p) 
         p.lds = lds;
         return true;
     };
-    // 1. small matrices with the row index: two half-waves per block (rows 0-3 / 4-7), two workgroups per CU
+    // 1. small matrices with the row index: four or two half-waves per block (rows 0-1 / 2-3 / 4-5 / 6-7 or rows
+    //    0-3 / 4-7), up to 32 half-waves (16 waves) per workgroup, two workgroups per CU
     if (index && rows) {
         const uint32_t G = std::max(1u, ceil_div(groups, 2u * ncu_)), blocks = G * CB;
         const uint32_t lds = blocks * kSlotWords0 * 4u + G * part;
-        if (2u * blocks <= 20u && lds <= kDynLdsPipe) return set(false, 2u, G, 2u * blocks, kSlotWords0, lds);
+        if (lds <= kDynLdsPipe) {
+            if (4u * blocks <= 32u) return set(false, 4u, G, 4u * blocks, kSlotWords0, lds);
+            if (2u * blocks <= 20u) return set(false, 2u, G, 2u * blocks, kSlotWords0, lds);
+        }
     }
     // 2. one block per half-wave, one round: two workgroups of up to 32 half-waves (16 waves) per CU, which the
     //    58-VGPR kernel allows (8 waves per SIMD)

@@ -162,8 +162,9 @@ __device__ __forceinline__ void bulk_commit(const Bulk &B, uint32_t *buf, const 
 // activations or, for dequantization, the eight BF16 pairs in pw.  A step whose table entries were not both fast in
 // some lane of the wave is redone code by code from its start by the whole wave (0.09% of lane-steps, 5% of
 // wave-steps for N(0, 0.02^2) BF16 at a 12-bit window).
-template <int ELEM, int MODE, bool XBF16>
-__device__ __forceinline__ float row0(Seq<ELEM> &S, const LutLds &s, const uint4 &rw, const XRegs<XBF16> &x, uint32_t pw[8]) {
+template <int ELEM, int MODE, bool XBF16, int STRIDE = 1>
+__device__ __forceinline__ float row0(Seq<ELEM, STRIDE> &S, const LutLds &s, const uint4 &rw, const XRegs<XBF16> &x,
+                                      uint32_t pw[8]) {
     float sum = 0.f;
 #pragma unroll
     for (int k = 0; k < 4; k++) {
@@ -209,7 +210,8 @@ __device__ __forceinline__ float rowsN(const LutLds &s, const uint32_t *lane, ui
     }
     if (MODE == kDequant || MODE == kRowIndex) return 0.f;
     if constexpr (NR == 8) return reduce8_transposed(acc, L);
-    else return reduce4_transposed(acc, L);
+    else if constexpr (NR == 4) return reduce4_transposed(acc, L);
+    else return reduce2_transposed(acc, L);
 }
 
 // rows0 for the pipelined kernel.  The raw-plane rows go through a ring of four registers (row r + 4 of this block
@@ -294,7 +296,8 @@ __device__ __forceinline__ float rowsN_global(const LutLds &s, const uint32_t *l
     }
     if (MODE == kDequant || MODE == kRowIndex) return 0.f;
     if constexpr (NR == 8) return reduce8_transposed(acc, L);
-    else return reduce4_transposed(acc, L);
+    else if constexpr (NR == 4) return reduce4_transposed(acc, L);
+    else return reduce2_transposed(acc, L);
 }
 
 // Layout 0.  A workgroup owns G whole row groups (nt = G * CB blocks) and works through them in rounds of H blocks,
@@ -306,7 +309,7 @@ __device__ __forceinline__ float rowsN_global(const LutLds &s, const uint32_t *l
 //     waits on global memory.  One barrier per round publishes the next region.
 template <int ELEM, int MODE, bool XBF16, bool PIPE, int NR>
 __global__ void __launch_bounds__(1024) k_layout0(BlockArgs a) {
-    static_assert(NR == 8 || (NR == 4 && !PIPE), "row splits only in the single-round kernel");
+    static_assert(NR == 8 || ((NR == 4 || NR == 2) && !PIPE), "row splits only in the single-round kernel");
     constexpr uint32_t SP = kRows0 / NR;                      // half-waves per block
     constexpr bool ROWS = MODE == kToken || MODE == kF32;     // modes that keep row sums
     __shared__ LutLds s;
@@ -343,7 +346,8 @@ __global__ void __launch_bounds__(1024) k_layout0(BlockArgs a) {
         lut_commit<kLutSeq>(s, Q, a.lut);
         uint4 raw[4];
 #pragma unroll
-        for (int r = 0; r < 4; r++) raw[r] = MODE == kRowIndex ? make_uint4(0u, 0u, 0u, 0u) : raw_row<ELEM>(a.low, f, c, r0 + r);
+        for (int r = 0; r < (NR < 4 ? NR : 4); r++)
+            raw[r] = MODE == kRowIndex ? make_uint4(0u, 0u, 0u, 0u) : raw_row<ELEM>(a.low, f, c, r0 + r);
         const bool fits = R.n16 * 4u <= cap;
         if (fits) bulk_commit(Bk, cur, R, tid, nth);
         __syncthreads();
@@ -621,6 +625,8 @@ static int launch_prefix_t(const LaunchPlan &p, const BlockArgs &a, hipStream_t 
         hipLaunchKernelGGL((k_layout0<ELEM, MODE, XBF16, true, 8>), dim3(p.grid), dim3(p.threads), p.lds, st, a);
     else if (p.layout == 0 && p.split == 2 && (MODE == kToken || MODE == kF32))
         hipLaunchKernelGGL((k_layout0<ELEM, MODE, XBF16, false, 4>), dim3(p.grid), dim3(p.threads), p.lds, st, a);
+    else if (p.layout == 0 && p.split == 4 && (MODE == kToken || MODE == kF32))
+        hipLaunchKernelGGL((k_layout0<ELEM, MODE, XBF16, false, 2>), dim3(p.grid), dim3(p.threads), p.lds, st, a);
     else if (p.layout == 0)
         hipLaunchKernelGGL((k_layout0<ELEM, MODE, XBF16, false, 8>), dim3(p.grid), dim3(p.threads), p.lds, st, a);
     else if constexpr (MODE != kRowIndex)

@@ -102,6 +102,18 @@ __device__ __forceinline__ float reduce4_transposed(float acc[4], uint32_t L) {
     return v;
 }
 
+// The same for 2 row sums: afterwards lane L with (L & 15) == 0 holds the sum of row L >> 4.
+__device__ __forceinline__ float reduce2_transposed(float acc[2], uint32_t L) {
+    const bool up = L & 16;
+    float send = up ? acc[0] : acc[1], keep = up ? acc[1] : acc[0];
+    float v = keep + xor_f<16>(send);
+    v += xor_f<8>(v);
+    v += xor_f<4>(v);
+    v += xor_f<2>(v);
+    v += xor_f<1>(v);
+    return v;
+}
+
 // ---- decode table in LDS ----
 // The stored 4096-word LUT is re-encoded once per workgroup.  Entries that are not two complete codes get bit 31 (slow
 // path); for the others byte 0 (c = bits of both codes, 4..12) becomes
@@ -258,8 +270,9 @@ struct Window {
 // from P are then alignbit(A, B, s).  An advance by c <= 24 bits moves at most one word, exactly when c > s:
 // A, B <- B, C, and the new C is read for the step after next, so no read of stream words lies on the dependency chain
 // of a step:  window -> table read (kLutSeq encoding) -> shift -> table read -> add -> test -> select -> window.
-// The words may live in LDS (staged streams) or global memory (fallback).
-template <int ELEM>
+// The words may live in LDS (staged streams) or global memory (fallback).  STRIDE is the distance in words between
+// consecutive words of a lane (1 for a lane stream stored contiguously; kLanes for 32 lanes interleaved word by word).
+template <int ELEM, int STRIDE = 1>
 struct Seq {
     const uint32_t *wp;
     uint32_t s;
@@ -268,19 +281,21 @@ struct Seq {
     // At P = 0, P - 1 = -1 lies in word -1, whose value is never used: shift 0 selects B, and any advance then moves
     // a word.  It is not read either (word -1 of a global stream may precede the allocation).
     __device__ __forceinline__ void init(const uint32_t *lane) {
-        wp = lane - 1;
+        wp = lane - STRIDE;
         s = 0;
-        A = 0u; B = lane[0]; C = lane[1];
+        A = 0u; B = lane[0]; C = lane[STRIDE];
     }
     // start at bit position P of the lane's stream (any P >= 0; P = 0 is init's case)
     __device__ __forceinline__ void init_at(const uint32_t *lane, uint32_t P) {
         const int32_t m = (int32_t)P - 1;
-        wp = lane + (m >> 5);
+        wp = lane + (m >> 5) * STRIDE;
         s = 31u - ((uint32_t)m & 31u);
         reload();
     }
     // the bit position of the next code
-    __device__ __forceinline__ uint32_t position(const uint32_t *lane) const { return (uint32_t)(wp - lane) * 32u + 32u - s; }
+    __device__ __forceinline__ uint32_t position(const uint32_t *lane) const {
+        return (uint32_t)((wp - lane) / STRIDE) * 32u + 32u - s;
+    }
     __device__ __forceinline__ uint32_t window() const { return __builtin_amdgcn_alignbit(A, B, s); }
     // t = s - c as an 8-bit two's complement value in its low byte (higher bits are don't-care)
     __device__ __forceinline__ void step(uint32_t t) {
@@ -288,11 +303,11 @@ struct Seq {
         s = t & 31u;
         A = crossed ? B : A;
         B = crossed ? C : B;
-        wp = crossed ? wp + 1 : wp;
-        C = wp[2];
+        wp = crossed ? wp + STRIDE : wp;
+        C = wp[2 * STRIDE];
     }
     // re-read the cached words after the position was reset; A is dead when s = 0 (see init), so it is not read then
-    __device__ __forceinline__ void reload() { A = wp[s == 0 ? 1 : 0]; B = wp[1]; C = wp[2]; }
+    __device__ __forceinline__ void reload() { A = wp[s == 0 ? STRIDE : 0]; B = wp[STRIDE]; C = wp[2 * STRIDE]; }
 
     // Four codes = two pairs from two table reads; e1 holds the exponent bytes of weights 0,1 in bytes 1,2 and e2
     // those of weights 2,3.  Correct only if neither entry has bit 31; otherwise the caller resets the position and

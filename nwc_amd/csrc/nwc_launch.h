@@ -7,7 +7,7 @@ namespace nwc {
 struct LaunchPlan {
     int layout;
     bool pipe;              // layout 0: rounds through two region buffers, the next round prefetched
-    uint32_t split;         // layout 0: half-waves per block (1, or 2 with the row index)
+    uint32_t split;         // layout 0: half-waves per block (1, or 2 or 4 with the row index)
     uint32_t grid, threads, lds, G;
     uint32_t slot_words;    // layout 0: region-buffer words per block
 };

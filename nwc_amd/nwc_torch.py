@@ -282,9 +282,9 @@ class NWCWeight:
 
     def token_bytes(self):
         """Algorithmic bytes one token-path call reads: the compressed matrix, plus the row-index entries the kernel
-        uses (64 bytes per block when it splits blocks over two half-waves)."""
+        uses: 64 bytes per block when it splits blocks over two half-waves (row 4's entries), 192 over four."""
         split = _lib.nwc_token_split(self.n, self.in_features, self.code, int(self.row_index() is not None))
-        return self.bytes + (self.bases.numel() * LANES * 2 if split == 2 else 0)
+        return self.bytes + self.bases.numel() * LANES * 2 * (split - 1)
 
     def linear_bf16(self, x: torch.Tensor, bias) -> torch.Tensor:
         """Token path: y = scale * (W x) + bias, x BF16 or fp32, y BF16."""

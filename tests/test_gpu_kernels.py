@@ -183,15 +183,25 @@ def test_row_index_values(cuda, M, K, escapes):
     assert np.array_equal(got[mask], want[mask])
 
 
-def test_token_path_with_and_without_row_index(cuda):
-    """The split decode (two half-waves per block, reduce over 4 rows) against the whole-block decode."""
-    import ctypes
+@pytest.mark.parametrize("M,K,split,escapes", [(2560, 4096, 4, "none"), (6144, 2560, 2, "none"), (1003, 1100, 4, "none"),
+                                               (2560, 4096, 4, "sparse"), (2560, 4096, 4, "dense"),
+                                               (6144, 2560, 2, "dense"), (1003, 1100, 4, "dense")])
+def test_token_path_with_and_without_row_index(cuda, M, K, split, escapes):
+    """The split decode (four or two half-waves per block, each reducing 2 or 4 rows) against the whole-block decode:
+    o_proj and qkv_proj shapes on 256 CUs, a ragged matrix, and escape runs (24-bit codes) dense enough that tiles do
+    not fit their LDS region and decode from global memory."""
     from nwc_amd.nwc_torch import _lib, _ptr, _stream
     NWCWeight, _, _ = _nwc()
-    M, K = 2560, 4096                                                  # o_proj: small enough for the split plan
-    w = bf16_matrix(M, K, seed=77, escapes=False)
+    w = bf16_matrix(M, K, seed=77, escapes=escapes == "sparse")
+    if escapes == "dense":                    # 24-bit codes: whole lanes of rows 0-7, 9, 13 and 16-23 are escapes
+        big = torch.tensor(1e30, dtype=torch.bfloat16)
+        w[0:8, 0:64] = big
+        w[9, 512:700] = -big
+        w[13, 1024:1100] = big
+        w[16:24, 16:32] = -big
     c = NWCWeight(w, device="cuda", layout=0)
-    assert _lib.nwc_token_split(c.n, K, c.code, 1) == 2
+    assert _lib.nwc_token_split(c.n, K, c.code, 1) == split
+    assert _lib.nwc_token_split(c.n, K, c.code, 0) == 1
     x = torch.randn(K, generator=torch.Generator().manual_seed(6)).to(torch.bfloat16).cuda()
     ys = []
     for ri in (c.row_index(), None):
