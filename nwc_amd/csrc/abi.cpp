@@ -104,11 +104,43 @@ bool plan_layout0(const Shape &f, int mode, int ncu, bool index, LaunchPlan &p) 
     }
 }
 
+// Layout 1, single round, for the token path with the row index: G whole 16-row groups per workgroup (two workgroups
+// per CU), SP = 4 or 2 half-waves per block, at most 32 half-waves; a region buffer of up to 880 words per block (a
+// 16 x 512 block of N(0, 0.02^2) BF16 needs ~700, real model weights ~760).  Building the index itself uses SP = 1
+// (decoding from global memory: the region is larger than the copy's four chunks per thread).  False otherwise: the
+// caller then uses the multi-block kernel.
+constexpr uint32_t kSlotWords1s = 880, kSlotWords1Min = 768;
+bool plan_layout1(const Shape &f, int mode, int ncu, bool index, LaunchPlan &p) {
+    p = LaunchPlan{};
+    p.layout = 1;
+    const bool rows = mode == kToken || mode == kF32;
+    const uint32_t CB = f.CB, groups = f.groups();
+    const uint32_t G = std::max(1u, (groups + 2u * (uint32_t)ncu - 1u) / (2u * (uint32_t)ncu)), blocks = G * CB;
+    for (uint32_t sp : {4u, 2u, 1u}) {
+        if (sp > 1 ? !(index && rows) : mode != kRowIndex) continue;
+        const uint32_t halves = (blocks * sp + 1u) & ~1u;
+        if (halves > 32u) continue;
+        const uint32_t part = rows ? G * kRows12 * CB * sp * 4u + (f.K16 + 31u) / 32u * 64u : 0u;   // + x as BF16
+        if (part + blocks * kSlotWords1Min * 4u > kDynLdsPipe) continue;
+        const uint32_t slot = std::min(kSlotWords1s, (kDynLdsPipe - part) / (4u * blocks));
+        p.split = sp;
+        p.G = G;
+        p.threads = 32u * halves;
+        p.grid = (groups + G - 1u) / G;
+        p.slot_words = slot;
+        p.lds = blocks * slot * 4u + part;
+        return true;
+    }
+    return false;
+}
+
 // Layouts 1/2: workgroup tile = G whole row groups, one block per half-wave where the LDS budget allows.  Prefer at
 // least two workgroups per CU (small matrices spread over the whole chip), at most 32 blocks (16 waves) per
 // workgroup, and an even block count so both halves of every wave have a block.
 bool plan_blocks(const Shape &f, int layout, int mode, int ncu, bool index, LaunchPlan &p) {
     if (layout == 0) return plan_layout0(f, mode, ncu, index, p);
+    if (layout == 1 && plan_layout1(f, mode, ncu, index, p)) return true;
+    if (mode == kRowIndex) return false;
     p = LaunchPlan{};
     p.layout = layout;
     const uint32_t CB = f.CB, groups = f.groups(), slot = slot_words_for(layout);
@@ -142,9 +174,9 @@ int run_blocks(int mode, bool xbf16, hipStream_t st, const uint8_t *data, const 
     const int layout = elem_layout(elem), t = elem_type(elem);
     const Shape f((uint32_t)(n / K), K, layout);
     LaunchPlan p;
-    if (!plan_blocks(f, layout, mode, ncu, aux != nullptr && layout == 0, p)) return -1;
+    if (!plan_blocks(f, layout, mode, ncu, aux != nullptr && layout <= 1, p)) return -1;
     BlockArgs a{data, bases, hdr, tab, low, x, bias, scale, out, aux, f.M, f.K, p.G,
-                layout == 0 ? p.slot_words : slot_words_for(layout)};
+                layout == 0 || p.split ? p.slot_words : slot_words_for(layout)};
     return layout == 2 ? launch_fixed(p, t, mode, xbf16, a, st) : launch_prefix(p, t, mode, xbf16, a, st);
 }
 
@@ -178,12 +210,12 @@ extern "C" int nwc_linear_xbf16(void *stream, const uint8_t *data, const uint32_
                                 const float *scale, uint16_t *y, uint64_t n, uint32_t K, int elem) {
     if (!shape_ok(n, kBlock, K, elem)) return -1;
     return run_blocks(kToken, true, (hipStream_t)stream, data, bases, hdr, tab, low, x, bias, scale, y, n, K, elem,
-                      elem_layout(elem) == 0 ? row_index : nullptr);
+                      elem_layout(elem) <= 1 ? row_index : nullptr);
 }
 
 extern "C" int nwc_row_index(void *stream, const uint8_t *data, const uint32_t *bases, const uint8_t *hdr, const uint32_t *tab,
                              const uint8_t *low, uint16_t *row_index, uint64_t n, uint32_t K, int elem) {
-    if (!shape_ok(n, kBlock, K, elem) || elem_layout(elem) != 0) return -1;
+    if (!shape_ok(n, kBlock, K, elem) || elem_layout(elem) > 1) return -1;
     return run_blocks(kRowIndex, true, (hipStream_t)stream, data, bases, hdr, tab, low, nullptr, nullptr, nullptr, row_index,
                       n, K, elem);
 }
@@ -194,8 +226,8 @@ extern "C" int nwc_token_split(uint64_t n, uint32_t K, int elem, int with_row_in
     if (ncu <= 0) return (int)hipErrorNoDevice;
     const Shape f((uint32_t)(n / K), K, elem_layout(elem));
     LaunchPlan p;
-    if (!plan_blocks(f, elem_layout(elem), kToken, ncu, with_row_index != 0 && elem_layout(elem) == 0, p)) return -1;
-    return elem_layout(elem) == 0 ? (int)p.split : 1;
+    if (!plan_blocks(f, elem_layout(elem), kToken, ncu, with_row_index != 0 && elem_layout(elem) <= 1, p)) return -1;
+    return elem_layout(elem) <= 1 && p.split ? (int)p.split : 1;
 }
 
 extern "C" int nwc_gather(void *stream, const uint8_t *data, const uint32_t *bases, const uint8_t *hdr, const uint32_t *tab,

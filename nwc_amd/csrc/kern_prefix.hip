@@ -511,6 +511,218 @@ __global__ void __launch_bounds__(1024) k_layout1(BlockArgs a) {
 }
 
 // ---------------------------------------------------------------------------------------------------------------
+// Layout 1, single round: a workgroup owns G whole 16-row groups (nt = G * CB <= H / SP blocks); their streams are
+// staged once into LDS like layout 0's, and each half-wave decodes super-chunks sc0 .. sc0 + NS - 1 of one block
+// (SP = 16 / NS half-waves per block; with SP > 1 the row index gives each lane's bit position at super-chunk
+// 4, 8, 12).  Raw super-chunks go through a ring of four registers (chunk s + 4 is requested when chunk s is done),
+// activations one super-chunk ahead.  Partial row sums are kept per (row, column block, part) and summed in a fixed
+// order by the workgroup.
+struct Coord1 {
+    uint32_t g, cb, b, rb, nsc;
+    uint32_t ro;                // byte offset in `low` of the lane's raw bytes of super-chunk 0 of the block
+};
+template <int ELEM>
+__device__ __forceinline__ Coord1 coord1(uint32_t t, uint32_t rg0, const Shape &f, uint32_t L) {
+    constexpr uint32_t RB = ELEM == kElemFp8 ? 8u : 16u;
+    Coord1 c;
+    c.g = t / f.CB;
+    c.cb = t - c.g * f.CB;
+    c.rb = rg0 + c.g;
+    c.b = c.rb * f.CB + c.cb;
+    c.nsc = c.cb == f.CB - 1u ? f.nsl : 16u;
+    c.ro = ((c.rb * f.spr + c.cb * 16u) * kLanes + L) * RB;
+    return c;
+}
+// Raw super-chunk sc of a block; past the block's last super-chunk it re-reads the last, so loads stay unconditional.
+// 32-bit offsets (the plane is below 4 GB: M * K16 < 2^32) keep one address register per load.
+template <int ELEM>
+__device__ __forceinline__ uint4 raw1(const uint8_t *__restrict__ low, const Coord1 &c, uint32_t sc) {
+    constexpr uint32_t RB = ELEM == kElemFp8 ? 8u : 16u;
+    return raw_slot1<ELEM>(low + (c.ro + min(sc, c.nsc - 1u) * (kLanes * RB)));
+}
+// Eight activations from kc as BF16 pairs (fp32 x: rounded to BF16, as the reference's fp32 path does for layouts
+// 1/2).  x holds K32 values, so every coded super-chunk is in bounds.
+template <bool XBF16>
+__device__ __forceinline__ uint4 x8_at(const void *x, uint32_t kc) {
+    if constexpr (XBF16) return *(const uint4 *)((const uint16_t *)x + kc);
+    const float4 a = ((const float4 *)((const float *)x + kc))[0], b = ((const float4 *)((const float *)x + kc))[1];
+    return make_uint4(f32_to_bf16_rne(a.x) | f32_to_bf16_rne(a.y) << 16, f32_to_bf16_rne(a.z) | f32_to_bf16_rne(a.w) << 16,
+                      f32_to_bf16_rne(b.x) | f32_to_bf16_rne(b.y) << 16, f32_to_bf16_rne(b.z) | f32_to_bf16_rne(b.w) << 16);
+}
+// The activations are staged once per workgroup as BF16 in LDS, so their per-super-chunk reads are LDS reads: a global
+// load there would be waited for in issue order together with the raw chunks requested before it.
+template <bool XBF16>
+__device__ __forceinline__ void stage_x1(uint4 *xs, const void *x, uint32_t n8, uint32_t tid, uint32_t nth) {
+    const uint32_t i0 = tid, i1 = tid + nth;
+    const uint4 v0 = x8_at<XBF16>(x, 8u * min(i0, n8 - 1u)), v1 = x8_at<XBF16>(x, 8u * min(i1, n8 - 1u));
+    if (i0 < n8) xs[i0] = v0;
+    if (i1 < n8) xs[i1] = v1;
+    for (uint32_t i = tid + 2u * nth; i < n8; i += nth) xs[i] = x8_at<XBF16>(x, 8u * i);
+}
+
+template <int ELEM, int MODE, int NS, bool FULL>
+__device__ __forceinline__ float2 chunks1(const LutLds &s, const uint32_t *lane, uint32_t P0, const BlockArgs &a,
+                                          const Shape &f, const uint4 *xs, uint4 ring[4], const Coord1 &c, uint32_t sc0,
+                                          uint32_t L) {
+    const uint32_t r = L >> 2, q = L & 3;
+    Seq<ELEM> S;
+    S.init_at(lane, P0);
+    float accA = 0.f, accB = 0.f;
+    const uint32_t kc0 = c.cb * kCols + 8u * q;
+#pragma unroll
+    for (int i = 0; i < NS; i++) {
+        const uint32_t sc = sc0 + i;
+        if (!FULL && sc >= c.nsc) break;                        // the last column block codes nsl super-chunks
+        if (MODE == kRowIndex && i > 0 && (i & 3) == 0)
+            ((uint16_t *)a.out)[((uint64_t)c.b * kRowIndexSplits + (i >> 2) - 1) * kLanes + L] = (uint16_t)S.position(lane);
+        uint4 xc = make_uint4(0u, 0u, 0u, 0u);
+        if (MODE == kToken || MODE == kF32) xc = xs[(kc0 + sc * 32u) >> 3];
+        const uint4 cw = ring[i & 3];
+        uint32_t pa[4], pb[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const uint32_t s0 = S.s;
+            const uint32_t *wp0 = S.wp;
+            uint32_t e1, e2;
+            S.fast_quad(s, e1, e2);
+            if (__any((int)(e1 | e2) < 0)) {
+                S.s = s0;
+                S.wp = wp0;
+                S.reload();
+                S.slow_quad(s, e1, e2);
+            }
+            const uint32_t rk = u4_get(cw, k);
+            if (MODE == kDequant) {
+                pa[k] = perm(e1, rk, kSelPair0);
+                pb[k] = perm(e2, rk, kSelPair2);
+                asm volatile("" : "+v"(pa[k]), "+v"(pb[k]));
+            } else if (MODE == kToken || MODE == kF32) {
+                const uint32_t xk = u4_get(xc, k);
+                accA = dot2_bf16(perm(e1, rk, kSelPair0), xk, accA);
+                accB = dot2_bf16(perm(e2, rk, kSelPair2), xk, accB);
+                asm volatile("" : "+v"(accA), "+v"(accB));
+            }
+        }
+        if (MODE != kRowIndex && i + 4 < NS) ring[i & 3] = raw1<ELEM>(a.low, c, sc + 4u);
+        if (MODE == kDequant) {
+            const uint32_t kc = kc0 + sc * 32u, row0 = c.rb * kRows12;
+            if (kc < f.K16) {                                   // a half super-chunk beyond K16 is filler
+                uint16_t *o = (uint16_t *)a.out + (uint64_t)row0 * f.K16 + kc;
+                if (row0 + r < f.M) *(uint4 *)(o + (uint64_t)r * f.K16) = make_uint4(pa[0], pa[1], pa[2], pa[3]);
+                if (row0 + r + 8 < f.M) *(uint4 *)(o + (uint64_t)(r + 8) * f.K16) = make_uint4(pb[0], pb[1], pb[2], pb[3]);
+            }
+        }
+    }
+    if (MODE == kRowIndex) {                                    // entries past the block's last super-chunk: its end
+        for (uint32_t j = (c.nsc + 3u) / 4u; j <= kRowIndexSplits; j++)
+            if (j >= 1u && 4u * j >= c.nsc)
+                ((uint16_t *)a.out)[((uint64_t)c.b * kRowIndexSplits + j - 1u) * kLanes + L] = (uint16_t)S.position(lane);
+    }
+    accA += xor_f<1>(accA); accA += xor_f<2>(accA);              // the four lanes of a row pair
+    accB += xor_f<1>(accB); accB += xor_f<2>(accB);
+    return make_float2(accA, accB);
+}
+
+// chunks1 for a block whose tile does not fit the region buffer (and for building the row index): from global memory,
+// with a rolled loop and one raw load per super-chunk (compact code for a rare path).
+template <int ELEM, int MODE, int NS>
+__device__ __forceinline__ float2 chunks1_global(const LutLds &s, const uint32_t *lane, uint32_t P0, const BlockArgs &a,
+                                                 const uint4 *xs, const Coord1 &c, uint32_t sc0, uint32_t L) {
+    Seq<ELEM> S;
+    S.init_at(lane, P0);
+    float accA = 0.f, accB = 0.f;
+    const uint32_t kc0 = c.cb * kCols + 8u * (L & 3);
+    const uint32_t sc1 = min(sc0 + NS, c.nsc);
+#pragma unroll 1
+    for (uint32_t sc = sc0; sc < sc1; sc++) {
+        if (MODE == kRowIndex && sc > 0 && (sc & 3) == 0)
+            ((uint16_t *)a.out)[((uint64_t)c.b * kRowIndexSplits + (sc >> 2) - 1) * kLanes + L] = (uint16_t)S.position(lane);
+        const uint4 cw = MODE == kRowIndex ? make_uint4(0u, 0u, 0u, 0u) : raw1<ELEM>(a.low, c, sc);
+        const uint4 xc = MODE == kToken || MODE == kF32 ? xs[(kc0 + sc * 32u) >> 3] : make_uint4(0u, 0u, 0u, 0u);
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const uint32_t s0 = S.s;
+            const uint32_t *wp0 = S.wp;
+            uint32_t e1, e2;
+            S.fast_quad(s, e1, e2);
+            if (__any((int)(e1 | e2) < 0)) {
+                S.s = s0;
+                S.wp = wp0;
+                S.reload();
+                S.slow_quad(s, e1, e2);
+            }
+            if (MODE == kToken || MODE == kF32) {
+                const uint32_t rk = u4_get(cw, k), xk = u4_get(xc, k);
+                accA = dot2_bf16(perm(e1, rk, kSelPair0), xk, accA);
+                accB = dot2_bf16(perm(e2, rk, kSelPair2), xk, accB);
+            }
+        }
+    }
+    if (MODE == kRowIndex) {                                    // entries past the block's last super-chunk: its end
+        for (uint32_t j = 1; j <= kRowIndexSplits; j++)
+            if (4u * j >= c.nsc)
+                ((uint16_t *)a.out)[((uint64_t)c.b * kRowIndexSplits + j - 1u) * kLanes + L] = (uint16_t)S.position(lane);
+    }
+    accA += xor_f<1>(accA); accA += xor_f<2>(accA);
+    accB += xor_f<1>(accB); accB += xor_f<2>(accB);
+    return make_float2(accA, accB);
+}
+
+template <int ELEM, int MODE, bool XBF16, int NS, bool FULL>
+__global__ void __launch_bounds__(1024) k_layout1s(BlockArgs a) {
+    constexpr uint32_t SP = 16u / NS;                          // half-waves per block
+    constexpr bool ROWS = MODE == kToken || MODE == kF32;
+    __shared__ LutLds s;
+    extern __shared__ uint32_t dyn[];
+    const uint32_t tid = threadIdx.x, nth = blockDim.x, L = tid & 31;
+    const uint32_t hw = tid >> 5, H = nth >> 5, HB = H / SP;
+    const uint32_t cap = a.slot_words * HB;
+    const Shape f(a.M, a.K, 1);
+    const uint32_t n8 = (f.K16 + 31u) / 32u * 4u;               // x: K32 BF16 values, in chunks of eight
+    uint32_t *cur = dyn;
+    uint4 *xs = (uint4 *)(dyn + cap);
+    float *part = (float *)(xs + (ROWS ? n8 : 0u));
+    const uint32_t rg0 = blockIdx.x * a.G;
+    const uint32_t ng = min(a.G, f.groups() - rg0);
+    const uint32_t nt = ng * f.CB, tl = nt - 1u;
+    const uint32_t B0 = rg0 * f.CB, nb = f.nb;
+    const uint32_t mend = B0 + nt == nb ? matrix_end(a, nb) : 0u;
+    Region R = region_of(a, B0, B0 + nt, nb, mend);
+    LutLoad Q;
+    lut_issue(Q, a.lut);
+    const uint32_t t = hw / SP, p = hw % SP, sc0 = p * NS;
+    const Coord1 c = coord1<ELEM>(min(t, tl), rg0, f, L);
+    const uint32_t n = a.hdr[(uint64_t)c.b * kHdrBytes + L], base = a.bases[c.b];
+    const uint32_t P0 = p ? a.aux[((uint64_t)c.b * kRowIndexSplits + sc0 / 4u - 1u) * kLanes + L] : 0u;
+    Bulk Bk;
+    bulk_issue(Bk, a.data, R, tid, nth);
+    if (ROWS) stage_x1<XBF16>(xs, a.x, n8, tid, nth);
+    lut_commit<kLutSeq>(s, Q, a.lut);
+    uint4 ring[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) ring[i] = MODE == kRowIndex ? make_uint4(0u, 0u, 0u, 0u) : raw1<ELEM>(a.low, c, sc0 + i);
+    // the copy moves four 16-byte chunks per thread (512 words per half-wave); a larger region (one half-wave per
+    // block, as when the row index is built) decodes from global memory
+    const bool fits = R.n16 <= 4u * nth && R.n16 * 4u <= cap;
+    if (fits) bulk_commit(Bk, cur, R, tid, nth);
+    __syncthreads();
+    if (t < nt) {
+        const uint32_t start = half_scan_incl(n, L) - n;
+        const uint32_t pi = ((c.g * kRows12 + (L >> 2)) * f.CB + c.cb) * SP + p;   // partial sum slot of row r
+        float2 v = make_float2(0.f, 0.f);
+        if (FULL || sc0 < c.nsc) {
+            if (fits) v = chunks1<ELEM, MODE, NS, FULL>(s, cur + ((base - R.lo16) >> 2) + start, P0, a, f, xs, ring, c, sc0, L);
+            else v = chunks1_global<ELEM, MODE, NS>(s, (const uint32_t *)(a.data + base) + start, P0, a, xs, c, sc0, L);
+        }
+        if (ROWS && (L & 3) == 0) {
+            part[pi] = v.x;
+            part[pi + 8u * f.CB * SP] = v.y;                   // row r + 8
+        }
+    }
+    if (ROWS) finish_rows<MODE>(a, part, rg0 * kRows12, ng * kRows12, f.CB * SP);
+}
+
+// ---------------------------------------------------------------------------------------------------------------
 // Row gather: one half-wave per requested row.  Layout 0 decodes and discards the rows in front of it inside each
 // column block; layout 1 decodes the whole 16-row group and the row's lanes store.
 template <int ELEM, typename P>
@@ -619,6 +831,32 @@ __global__ void __launch_bounds__(256) k_gather1(GatherArgs a) {
 }
 
 // ---------------------------------------------------------------------------------------------------------------
+// Layout 1, single round: FULL when every block codes all 16 super-chunks (K a multiple of 512).
+template <int ELEM, int MODE, bool XBF16>
+static int launch_layout1s(const LaunchPlan &p, const BlockArgs &a, hipStream_t st) {
+    const bool full = Shape(a.M, a.K, 1).nsl == 16u;
+    const dim3 g(p.grid), b(p.threads);
+    if constexpr (MODE == kToken && XBF16) {                   // the entry point that takes the row index
+        if (p.split == 4) {
+            if (full) hipLaunchKernelGGL((k_layout1s<ELEM, MODE, XBF16, 4, true>), g, b, p.lds, st, a);
+            else hipLaunchKernelGGL((k_layout1s<ELEM, MODE, XBF16, 4, false>), g, b, p.lds, st, a);
+            return (int)hipGetLastError();
+        }
+        if (p.split == 2) {
+            if (full) hipLaunchKernelGGL((k_layout1s<ELEM, MODE, XBF16, 8, true>), g, b, p.lds, st, a);
+            else hipLaunchKernelGGL((k_layout1s<ELEM, MODE, XBF16, 8, false>), g, b, p.lds, st, a);
+            return (int)hipGetLastError();
+        }
+    }
+    if constexpr (MODE == kRowIndex) {
+        if (p.split != 1) return -1;
+        if (full) hipLaunchKernelGGL((k_layout1s<ELEM, MODE, XBF16, 16, true>), g, b, p.lds, st, a);
+        else hipLaunchKernelGGL((k_layout1s<ELEM, MODE, XBF16, 16, false>), g, b, p.lds, st, a);
+        return (int)hipGetLastError();
+    }
+    return -1;
+}
+
 template <int ELEM, int MODE, bool XBF16>
 static int launch_prefix_t(const LaunchPlan &p, const BlockArgs &a, hipStream_t st) {
     if (p.layout == 0 && p.pipe)
@@ -629,6 +867,8 @@ static int launch_prefix_t(const LaunchPlan &p, const BlockArgs &a, hipStream_t 
         hipLaunchKernelGGL((k_layout0<ELEM, MODE, XBF16, false, 2>), dim3(p.grid), dim3(p.threads), p.lds, st, a);
     else if (p.layout == 0)
         hipLaunchKernelGGL((k_layout0<ELEM, MODE, XBF16, false, 8>), dim3(p.grid), dim3(p.threads), p.lds, st, a);
+    else if (p.layout == 1 && p.split)
+        return launch_layout1s<ELEM, MODE, XBF16>(p, a, st);
     else if constexpr (MODE != kRowIndex)
         hipLaunchKernelGGL((k_layout1<ELEM, MODE, XBF16>), dim3(p.grid), dim3(p.threads), p.lds, st, a);
     else

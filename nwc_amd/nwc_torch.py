@@ -61,7 +61,7 @@ _lib.nwc_linear_xbf16.restype = I32
 _lib.nwc_linear_xbf16.argtypes = [P, P, P, P, P, P, P, P, P, P, P, U64, U32, I32]
 _lib.nwc_row_index.restype = I32; _lib.nwc_row_index.argtypes = [P, P, P, P, P, P, P, U64, U32, I32]
 _lib.nwc_token_split.restype = I32; _lib.nwc_token_split.argtypes = [U64, U32, I32, I32]
-ROW_INDEX = os.environ.get("NWC_ROW_INDEX", "1") != "0"   # layout 0: build the row index for the token path
+ROW_INDEX = os.environ.get("NWC_ROW_INDEX", "1") != "0"   # layouts 0/1: build the row index for the token path
 _lib.nwc_gather.restype = I32; _lib.nwc_gather.argtypes = [P, P, P, P, P, P, P, U32, P, U64, U32, U32, I32]
 _lib.nwc_ref_fp8.restype = I32; _lib.nwc_ref_fp8.argtypes = [P, P, P, P, P, U64, U32]
 _lib.nwc_setup.restype = I32; _lib.nwc_setup.argtypes = []
@@ -265,9 +265,11 @@ class NWCWeight:
         return y if self.scale is None else y * self.scale
 
     def row_index(self):
-        """Layout-0 row index (uint16 [blocks x 3 x 32], built on the GPU on first use; not part of the format): lets
-        the token kernel decode a block's rows 0-3 and 4-7 on two half-waves.  None for layouts 1/2 or NWC_ROW_INDEX=0."""
-        if self.layout != 0 or not ROW_INDEX:
+        """Row index (uint16 [blocks x 3 x 32], built on the GPU on first use; not part of the format): each lane's bit
+        position at rows 2, 4, 6 (layout 0) or super-chunks 4, 8, 12 (layout 1), so the token kernel can split a block
+        over two or four half-waves.  None for layout 2, for layout-1 shapes whose index kernel has no single-round
+        plan (K > 16384), or with NWC_ROW_INDEX=0."""
+        if self.layout > 1 or not ROW_INDEX:
             return None
         ri = getattr(self, "_row_index", None)
         if ri is None:
@@ -275,14 +277,16 @@ class NWCWeight:
             ri = torch.empty(self.bases.numel() * 3 * LANES, dtype=torch.int16, device=self.data.device)
             err = _lib.nwc_row_index(_stream(), _ptr(self.data), _ptr(self.bases), _ptr(self.hdr), _ptr(self.lut),
                                      _ptr(self.low), _ptr(ri), self.n, self.in_features, self.code)
-            if err:
+            if err == -1 and self.layout == 1:
+                ri = False                                         # no plan for this shape: decode without an index
+            elif err:
                 raise RuntimeError(f"nwc_row_index error {err}")
             self._row_index = ri
-        return ri
+        return ri if ri is not False else None
 
     def token_bytes(self):
         """Algorithmic bytes one token-path call reads: the compressed matrix, plus the row-index entries the kernel
-        uses: 64 bytes per block when it splits blocks over two half-waves (row 4's entries), 192 over four."""
+        uses: 64 bytes per block when it splits blocks over two half-waves (the middle entries), 192 over four."""
         split = _lib.nwc_token_split(self.n, self.in_features, self.code, int(self.row_index() is not None))
         return self.bytes + self.bases.numel() * LANES * 2 * (split - 1)
 

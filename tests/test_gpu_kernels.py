@@ -170,6 +170,59 @@ def _row_index_cpu(w, lut):
     return pos.transpose(0, 2, 1, 3).reshape(-1, 3, 32), K16           # [block = group * CB + cb][j][lane]
 
 
+def _code_lengths(w, lut, rows):
+    """Code length of every weight, padded to whole row groups and column blocks (fillers: 2 bits)."""
+    M, K = w.shape
+    CB = (K + 511) // 512
+    Mp = (M + rows - 1) // rows * rows
+    hb = np.zeros((Mp, CB * 512), np.int64)
+    hb[:M, :K] = (bits16(w).reshape(M, K).astype(np.int64) >> 8) & 0x7F
+    lut = lut.astype(np.uint32)
+    eor = []
+    for q in range(15):
+        src = (1 << (11 - q)) if q < 11 else (q - 11) >> 1
+        sh = 8 if (q < 11 or (q & 1)) else 16
+        eor.append(int((lut[src] >> sh) & 0x7F))
+    rank = np.full(128, 15)
+    for r in range(14, -1, -1):
+        rank[eor[r]] = r
+    ln = np.where(rank[hb] < 15, rank[hb] + 2, 24)
+    ln[M:, :] = 2
+    ln[:, K:] = 2
+    return ln
+
+
+def _row_index_cpu_l1(w, lut):
+    """Bit positions of super-chunks 4, 8, 12 in every layout-1 lane stream (lane L = (r, q) codes, per super-chunk,
+    16 weights of rows r and r + 8: docs/format.md section 4c), or the lane's end where the block codes fewer."""
+    M, K = w.shape
+    K16, CB = (K + 15) // 16 * 16, (K + 511) // 512
+    nsl = ((K16 - (CB - 1) * 512) // 16 + 1) // 2
+    ln = _code_lengths(w, lut, 16)
+    G = ln.shape[0] // 16
+    L5 = ln.reshape(G, 16, CB, 16, 32)                                 # [group, row, block column, super-chunk, column]
+    bits = np.zeros((G, CB, 16, 8, 4), np.int64)                       # [group, cb, sc, r, q]
+    for j in range(16):
+        roff = 8 * ((j >> 1) & 1)
+        coff = 4 * ((j >> 3) & 1) + 2 * ((j >> 2) & 1) + (j & 1)
+        for q in range(4):
+            bits[:, :, :, :, q] += L5[:, roff:roff + 8, :, :, 8 * q + coff].transpose(0, 2, 3, 1)
+    bits[:, CB - 1, nsl:] = 0                                          # super-chunks the last block does not code
+    cum = np.cumsum(bits, axis=2).reshape(G, CB, 16, 32)               # after super-chunks 0..sc, lane 4r + q
+    pos = cum[:, :, [3, 7, 11], :]
+    return pos.reshape(-1, 3, 32)
+
+
+@pytest.mark.parametrize("M,K,escapes", [(64, 2048, False), (100, 1000, True), (13, 40, True), (300, 2560, False)])
+def test_row_index_values_layout1(cuda, M, K, escapes):
+    NWCWeight, _, _ = _nwc()
+    w = bf16_matrix(M, K, seed=M + K + 1, escapes=escapes)
+    c = NWCWeight(w, device="cuda", layout=1)
+    got = c.row_index().cpu().numpy().view(np.uint16).reshape(-1, 3, 32).astype(np.int64)
+    want = _row_index_cpu_l1(w, c.lut.cpu().numpy().view(np.uint32))
+    assert np.array_equal(got, want)
+
+
 @pytest.mark.parametrize("M,K,escapes", [(64, 2048, False), (100, 1000, True), (13, 40, True), (300, 2560, False)])
 def test_row_index_values(cuda, M, K, escapes):
     NWCWeight, _, _ = _nwc()
@@ -183,13 +236,16 @@ def test_row_index_values(cuda, M, K, escapes):
     assert np.array_equal(got[mask], want[mask])
 
 
-@pytest.mark.parametrize("M,K,split,escapes", [(2560, 4096, 4, "none"), (6144, 2560, 2, "none"), (1003, 1100, 4, "none"),
-                                               (2560, 4096, 4, "sparse"), (2560, 4096, 4, "dense"),
-                                               (6144, 2560, 2, "dense"), (1003, 1100, 4, "dense")])
-def test_token_path_with_and_without_row_index(cuda, M, K, split, escapes):
-    """The split decode (four or two half-waves per block, each reducing 2 or 4 rows) against the whole-block decode:
-    o_proj and qkv_proj shapes on 256 CUs, a ragged matrix, and escape runs (24-bit codes) dense enough that tiles do
-    not fit their LDS region and decode from global memory."""
+@pytest.mark.parametrize("layout,M,K,split,escapes", [
+    (0, 2560, 4096, 4, "none"), (0, 6144, 2560, 2, "none"), (0, 1003, 1100, 4, "none"), (0, 2560, 4096, 4, "sparse"),
+    (0, 2560, 4096, 4, "dense"), (0, 6144, 2560, 2, "dense"), (0, 1003, 1100, 4, "dense"),
+    (1, 2560, 4096, 4, "none"), (1, 6144, 2560, 4, "none"), (1, 19456, 2560, 2, "none"), (1, 1003, 1100, 4, "none"),
+    (1, 2560, 4096, 4, "dense"), (1, 1003, 1100, 4, "dense")])
+def test_token_path_with_and_without_row_index(cuda, layout, M, K, split, escapes):
+    """The split decode (layout 0: four or two half-waves per block, each reducing 2 or 4 rows; layout 1: super-chunk
+    ranges 4 or 8 long) against the whole-block decode: o_proj, qkv_proj and gate_up shapes on 256 CUs, a ragged
+    matrix (layout 1: a last column block of three super-chunks), and escape runs (24-bit codes) dense enough that tiles
+    do not fit their LDS region and decode from global memory."""
     from nwc_amd.nwc_torch import _lib, _ptr, _stream
     NWCWeight, _, _ = _nwc()
     w = bf16_matrix(M, K, seed=77, escapes=escapes == "sparse")
@@ -199,15 +255,16 @@ def test_token_path_with_and_without_row_index(cuda, M, K, split, escapes):
         w[9, 512:700] = -big
         w[13, 1024:1100] = big
         w[16:24, 16:32] = -big
-    c = NWCWeight(w, device="cuda", layout=0)
+    c = NWCWeight(w, device="cuda", layout=layout)
     assert _lib.nwc_token_split(c.n, K, c.code, 1) == split
     assert _lib.nwc_token_split(c.n, K, c.code, 0) == 1
     x = torch.randn(K, generator=torch.Generator().manual_seed(6)).to(torch.bfloat16).cuda()
+    xin = c._x16(x).contiguous()                             # zero-padded to K16 (layout 0) or K32 (layout 1)
     ys = []
     for ri in (c.row_index(), None):
         y = torch.empty(M, dtype=torch.bfloat16, device="cuda")
         err = _lib.nwc_linear_xbf16(_stream(), _ptr(c.data), _ptr(c.bases), _ptr(c.hdr), _ptr(c.lut), _ptr(c.low),
-                                    _ptr(ri) if ri is not None else None, _ptr(x), None, None, _ptr(y), c.n, K, c.code)
+                                    _ptr(ri) if ri is not None else None, _ptr(xin), None, None, _ptr(y), c.n, K, c.code)
         assert err == 0
         ys.append(y.double().cpu().numpy())
     y64 = (w.cuda().double() @ x.double()).cpu().numpy()
