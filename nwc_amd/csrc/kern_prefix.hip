@@ -171,8 +171,7 @@ __device__ __forceinline__ float row0(Seq<ELEM, STRIDE> &S, const LutLds &s, con
         const uint32_t s0 = S.s;
         const uint32_t *wp0 = S.wp;
         uint32_t e1, e2;
-        S.fast_quad(s, e1, e2);
-        if (__any((int)(e1 | e2) < 0)) {
+        if (__any(S.fast_quad(s, e1, e2) >= kSeqSlowTest)) {
             S.s = s0;
             S.wp = wp0;
             S.reload();
@@ -584,8 +583,7 @@ __device__ __forceinline__ float2 chunks1(const LutLds &s, const uint32_t *lane,
             const uint32_t s0 = S.s;
             const uint32_t *wp0 = S.wp;
             uint32_t e1, e2;
-            S.fast_quad(s, e1, e2);
-            if (__any((int)(e1 | e2) < 0)) {
+            if (__any(S.fast_quad(s, e1, e2) >= kSeqSlowTest)) {
                 S.s = s0;
                 S.wp = wp0;
                 S.reload();
@@ -644,8 +642,7 @@ __device__ __forceinline__ float2 chunks1_global(const LutLds &s, const uint32_t
             const uint32_t s0 = S.s;
             const uint32_t *wp0 = S.wp;
             uint32_t e1, e2;
-            S.fast_quad(s, e1, e2);
-            if (__any((int)(e1 | e2) < 0)) {
+            if (__any(S.fast_quad(s, e1, e2) >= kSeqSlowTest)) {
                 S.s = s0;
                 S.wp = wp0;
                 S.reload();

@@ -115,13 +115,17 @@ __device__ __forceinline__ float reduce2_transposed(float acc[2], uint32_t L) {
 }
 
 // ---- decode table in LDS ----
-// The stored 4096-word LUT is re-encoded once per workgroup.  Entries that are not two complete codes get bit 31 (slow
-// path); for the others byte 0 (c = bits of both codes, 4..12) becomes
+// The stored 4096-word LUT is re-encoded once per workgroup.  For entries that are two complete codes byte 0 (c = bits
+// of both codes, 4..12) becomes
 //   kLutWindow: 32 - c, the funnel shift that advances a register window by c (Window);
 //   kLutSeq:    18 - c, the right shift that puts the second code pair's 12 bits at [13:2] (Seq); two entries added
 //               give 36 - (c1 + c2) in byte 0.
-// Bytes 1/2 keep the two exponent bytes.
+// Bytes 1/2 keep the two exponent bytes and byte 3 is 0.  The other entries (slow path) become: kLutWindow, the stored
+// entry with bit 31; kLutSeq, exactly kSeqSlow, so that a step's sum e1 + e2 + s - 36 is at least kSeqSlowTest when
+// either entry is slow and below it when both are fast (their bytes sum to less than 2^26; the only exception, an
+// all-zero pair of exponent bytes with a borrow out of byte 0, reads as slow and is merely redone).
 enum LutKind { kLutWindow = 0, kLutSeq = 1 };
+constexpr uint32_t kSeqSlow = 0x40000000u, kSeqSlowTest = 0x20000000u;
 
 struct LutLds {
     uint32_t tab[kLutWords];
@@ -130,7 +134,7 @@ struct LutLds {
 
 template <int KIND>
 __device__ __forceinline__ uint32_t lut_transform(uint32_t e) {
-    if (e & kFlag) return e | 0x80000000u;
+    if (e & kFlag) return KIND == kLutWindow ? e | 0x80000000u : kSeqSlow;
     const uint32_t c = e & 0xFFu;
     return (e & 0xFFFFFF00u) | (KIND == kLutWindow ? ((32u - c) & 31u) : (18u - c));
 }
@@ -297,27 +301,31 @@ struct Seq {
         return (uint32_t)((wp - lane) / STRIDE) * 32u + 32u - s;
     }
     __device__ __forceinline__ uint32_t window() const { return __builtin_amdgcn_alignbit(A, B, s); }
-    // t = s - c as an 8-bit two's complement value in its low byte (higher bits are don't-care)
+    // t = s - c as an 8-bit two's complement value in its low byte (higher bits are don't-care); bit 7 says the
+    // cursor crossed into the next word
     __device__ __forceinline__ void step(uint32_t t) {
-        const bool crossed = (t & 0x80u) != 0;
+        const uint32_t x = __builtin_amdgcn_ubfe(t, 7, 1);
+        const bool crossed = x != 0u;
         s = t & 31u;
         A = crossed ? B : A;
         B = crossed ? C : B;
-        wp = crossed ? wp + STRIDE : wp;
+        wp += x * STRIDE;
         C = wp[2 * STRIDE];
     }
     // re-read the cached words after the position was reset; A is dead when s = 0 (see init), so it is not read then
     __device__ __forceinline__ void reload() { A = wp[s == 0 ? STRIDE : 0]; B = wp[STRIDE]; C = wp[2 * STRIDE]; }
 
     // Four codes = two pairs from two table reads; e1 holds the exponent bytes of weights 0,1 in bytes 1,2 and e2
-    // those of weights 2,3.  Correct only if neither entry has bit 31; otherwise the caller resets the position and
-    // redoes the step with slow_quad.  Byte 0 of e1 + e2 is 36 - c (kLutSeq), so e1 + e2 + s - 36 has s - c in its low
-    // byte (bytes 1-3 hold exponent sums and do not matter).
-    __device__ __forceinline__ void fast_quad(const LutLds &T, uint32_t &e1, uint32_t &e2) {
+    // those of weights 2,3.  Byte 0 of e1 + e2 is 36 - c (kLutSeq), so t = e1 + e2 + s - 36 has s - c in its low byte
+    // (bytes 1-3 hold exponent sums and do not matter).  Returns t: the step is correct only if t < kSeqSlowTest;
+    // otherwise the caller resets the position and redoes the step with slow_quad.
+    __device__ __forceinline__ uint32_t fast_quad(const LutLds &T, uint32_t &e1, uint32_t &e2) {
         const uint32_t hi = window();
         e1 = lds_entry(T, (hi >> 18) & 0x3FFCu);
         e2 = lds_entry(T, (hi >> (e1 & 31u)) & 0x3FFCu);               // the 12 bits after the first c1
-        step(e1 + e2 + (s - 36u));
+        const uint32_t t = e1 + e2 + (s - 36u);
+        step(t);
+        return t;
     }
 
     // one code by counting leading zeros: rank r < max -> r zeros, one, sign; BF16 escape -> 15 zeros, one, byte
@@ -336,9 +344,9 @@ struct Seq {
         return b;
     }
     __device__ __forceinline__ void slow_quad(const LutLds &T, uint32_t &e1, uint32_t &e2) {
-        uint32_t bytes = 0;                                            // b3 b2 b1 b0 after four codes
+        uint32_t bytes = slow_code(T) << 24;                           // b3 b2 b1 b0 after four codes
 #pragma unroll 1
-        for (int k = 0; k < 4; k++) bytes = (bytes >> 8) | (slow_code(T) << 24);
+        for (int k = 1; k < 4; k++) bytes = (bytes >> 8) | (slow_code(T) << 24);
         e1 = (bytes << 8) & 0x00FFFF00u;
         e2 = (bytes >> 8) & 0x00FFFF00u;
     }
