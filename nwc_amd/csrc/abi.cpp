@@ -110,6 +110,7 @@ bool plan_layout0(const Shape &f, int mode, int ncu, bool index, LaunchPlan &p) 
 // (decoding from global memory: the region is larger than the copy's four chunks per thread).  False otherwise: the
 // caller then uses the multi-block kernel.
 constexpr uint32_t kSlotWords1s = 880, kSlotWords1Min = 768;
+constexpr uint32_t kDynLdsOne = 128u * 1024u;         // dynamic LDS of a workgroup that has its CU to itself
 bool plan_layout1(const Shape &f, int mode, int ncu, bool index, LaunchPlan &p) {
     p = LaunchPlan{};
     p.layout = 1;
@@ -130,6 +131,22 @@ bool plan_layout1(const Shape &f, int mode, int ncu, bool index, LaunchPlan &p) 
         p.slot_words = slot;
         p.lds = blocks * slot * 4u + part;
         return true;
+    }
+    // several items per half-wave: one 16-row group per workgroup, 32 half-waves, up to kDynLdsOne of LDS (one such
+    // workgroup per CU; the region copy moves at most 64 KB)
+    if (index && mode == kToken && CB * 4u > 32u) {
+        const uint32_t part = kRows12 * CB * 4u * 4u + (f.K16 + 31u) / 32u * 64u;
+        const uint32_t slot = std::min(kSlotWords1s, (kDynLdsOne - part) / (4u * CB));
+        if (slot >= kSlotWords1Min && CB * kSlotWords1Min * 4u <= 64u * 1024u) {
+            p.split = 4;
+            p.multi = true;
+            p.G = 1;
+            p.threads = 1024;
+            p.grid = groups;
+            p.slot_words = slot;
+            p.lds = CB * slot * 4u + part;
+            return true;
+        }
     }
     return false;
 }

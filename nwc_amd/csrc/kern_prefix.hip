@@ -559,10 +559,12 @@ __device__ __forceinline__ void stage_x1(uint4 *xs, const void *x, uint32_t n8, 
     for (uint32_t i = tid + 2u * nth; i < n8; i += nth) xs[i] = x8_at<XBF16>(x, 8u * i);
 }
 
-template <int ELEM, int MODE, int NS, bool FULL>
+// NEXT (NS = 4, several items per half-wave): each ring slot is refilled with the next item's super-chunk once used.
+template <int ELEM, int MODE, int NS, bool FULL, bool NEXT = false>
 __device__ __forceinline__ float2 chunks1(const LutLds &s, const uint32_t *lane, uint32_t P0, const BlockArgs &a,
                                           const Shape &f, const uint4 *xs, uint4 ring[4], const Coord1 &c, uint32_t sc0,
-                                          uint32_t L) {
+                                          uint32_t L, const Coord1 *cn = nullptr, uint32_t nsc0 = 0) {
+    static_assert(!NEXT || NS == 4, "next-item refills for four-super-chunk items");
     const uint32_t r = L >> 2, q = L & 3;
     Seq<ELEM> S;
     S.init_at(lane, P0);
@@ -601,7 +603,8 @@ __device__ __forceinline__ float2 chunks1(const LutLds &s, const uint32_t *lane,
                 asm volatile("" : "+v"(accA), "+v"(accB));
             }
         }
-        if (MODE != kRowIndex && i + 4 < NS) ring[i & 3] = raw1<ELEM>(a.low, c, sc + 4u);
+        if constexpr (NEXT) ring[i & 3] = raw1<ELEM>(a.low, *cn, nsc0 + i);
+        else if (MODE != kRowIndex && i + 4 < NS) ring[i & 3] = raw1<ELEM>(a.low, c, sc + 4u);
         if (MODE == kDequant) {
             const uint32_t kc = kc0 + sc * 32u, row0 = c.rb * kRows12;
             if (kc < f.K16) {                                   // a half super-chunk beyond K16 is filler
@@ -719,6 +722,92 @@ __global__ void __launch_bounds__(1024) k_layout1s(BlockArgs a) {
     if (ROWS) finish_rows<MODE>(a, part, rg0 * kRows12, ng * kRows12, f.CB * SP);
 }
 
+// Layout 1, several items per half-wave: for matrices whose row groups hold more blocks than a workgroup has
+// half-waves at two per block (K > 8192, e.g. 2560 x 9728: 19 blocks per 16-row group).  A workgroup owns one 16-row
+// group (its streams staged once, up to ~90 KB of LDS), and its items (block, quarter of the super-chunks) go
+// round-robin to 32 half-waves; while an item decodes, the next item's raw super-chunks, header byte, base and
+// row-index entry are requested, so a half-wave never waits for global memory between items.
+template <int ELEM, bool FULL>
+__global__ void __launch_bounds__(1024) k_layout1m(BlockArgs a) {
+    constexpr int MODE = kToken;
+    constexpr uint32_t NS = 4, SP = 4;
+    __shared__ LutLds s;
+    extern __shared__ uint32_t dyn[];
+    const uint32_t tid = threadIdx.x, nth = blockDim.x, L = tid & 31;
+    const uint32_t hw = tid >> 5, H = nth >> 5;
+    const Shape f(a.M, a.K, 1);
+    const uint32_t rg0 = blockIdx.x * a.G;
+    const uint32_t ng = min(a.G, f.groups() - rg0);
+    const uint32_t nt = ng * f.CB;
+    const uint32_t cap = a.slot_words * a.G * f.CB;
+    const uint32_t n8 = (f.K16 + 31u) / 32u * 4u;
+    uint32_t *cur = dyn;
+    uint4 *xs = (uint4 *)(dyn + cap);
+    float *part = (float *)(xs + n8);
+    const uint32_t B0 = rg0 * f.CB, nb = f.nb;
+    const uint32_t mend = B0 + nt == nb ? matrix_end(a, nb) : 0u;
+    Region R = region_of(a, B0, B0 + nt, nb, mend);
+    LutLoad Q;
+    lut_issue(Q, a.lut);
+    const uint32_t ntot = nt * SP, itl = ntot - 1u;
+    auto item = [&](uint32_t it, Coord1 &c, uint32_t &p) {
+        const uint32_t i = min(it, itl);
+        c = coord1<ELEM>(i / SP, rg0, f, L);
+        p = i % SP;
+    };
+    Coord1 c;
+    uint32_t p;
+    item(hw, c, p);
+    uint32_t n = a.hdr[c.b * kHdrBytes + L], base = a.bases[c.b];
+    uint32_t P0 = p ? a.aux[(c.b * kRowIndexSplits + p - 1u) * kLanes + L] : 0u;
+    Bulk Bk;
+    bulk_issue(Bk, a.data, R, tid, nth);
+    stage_x1<true>(xs, a.x, n8, tid, nth);
+    lut_commit<kLutSeq>(s, Q, a.lut);
+    uint4 ring[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) ring[i] = raw1<ELEM>(a.low, c, p * NS + i);
+    const bool fits = R.n16 <= 4u * nth && R.n16 * 4u <= cap;
+    if (fits) bulk_commit(Bk, cur, R, tid, nth);
+    __syncthreads();
+    // trip count of the wave (both halves run it; a half without an item decodes a copy of the last and stores nothing)
+    const uint32_t hw0 = hw & ~1u;
+    const uint32_t nk = ntot > hw0 ? (ntot - hw0 + H - 1u) / H : 0u;
+    uint32_t it = hw;
+    for (uint32_t k = 0; k < nk; k++) {
+        Coord1 cn;
+        uint32_t pn;
+        item(it + H, cn, pn);
+        const uint32_t nn = a.hdr[cn.b * kHdrBytes + L], basen = a.bases[cn.b];
+        const uint32_t P0n = pn ? a.aux[(cn.b * kRowIndexSplits + pn - 1u) * kLanes + L] : 0u;
+        const uint32_t start = half_scan_incl(n, L) - n, sc0 = p * NS;
+        float2 v = make_float2(0.f, 0.f);
+        if (FULL || sc0 < c.nsc) {
+            if (fits)
+                v = chunks1<ELEM, MODE, NS, FULL, true>(s, cur + ((base - R.lo16) >> 2) + start, P0, a, f, xs, ring, c, sc0, L,
+                                                        &cn, pn * NS);
+            else
+                v = chunks1_global<ELEM, MODE, NS>(s, (const uint32_t *)(a.data + base) + start, P0, a, xs, c, sc0, L);
+        }
+        if (!fits || !(FULL || sc0 < c.nsc)) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) ring[i] = raw1<ELEM>(a.low, cn, pn * NS + i);
+        }
+        if (it < ntot && (L & 3) == 0) {
+            const uint32_t pi = ((c.g * kRows12 + (L >> 2)) * f.CB + c.cb) * SP + p;
+            part[pi] = v.x;
+            part[pi + 8u * f.CB * SP] = v.y;
+        }
+        it += H;
+        c = cn;
+        p = pn;
+        n = nn;
+        base = basen;
+        P0 = P0n;
+    }
+    finish_rows<MODE>(a, part, rg0 * kRows12, ng * kRows12, f.CB * SP);
+}
+
 // ---------------------------------------------------------------------------------------------------------------
 // Row gather: one half-wave per requested row.  Layout 0 decodes and discards the rows in front of it inside each
 // column block; layout 1 decodes the whole 16-row group and the row's lanes store.
@@ -834,6 +923,17 @@ static int launch_layout1s(const LaunchPlan &p, const BlockArgs &a, hipStream_t 
     const bool full = Shape(a.M, a.K, 1).nsl == 16u;
     const dim3 g(p.grid), b(p.threads);
     if constexpr (MODE == kToken && XBF16) {                   // the entry point that takes the row index
+        if (p.multi) {
+            // more than 64 KB of dynamic LDS: raise the kernel's limit (idempotent, so concurrent first calls are fine)
+            auto kf = full ? (const void *)k_layout1m<ELEM, true> : (const void *)k_layout1m<ELEM, false>;
+            if (p.lds > 64u * 1024u) {
+                const hipError_t e = hipFuncSetAttribute(kf, hipFuncAttributeMaxDynamicSharedMemorySize, (int)p.lds);
+                if (e != hipSuccess) return (int)e;
+            }
+            if (full) hipLaunchKernelGGL((k_layout1m<ELEM, true>), g, b, p.lds, st, a);
+            else hipLaunchKernelGGL((k_layout1m<ELEM, false>), g, b, p.lds, st, a);
+            return (int)hipGetLastError();
+        }
         if (p.split == 4) {
             if (full) hipLaunchKernelGGL((k_layout1s<ELEM, MODE, XBF16, 4, true>), g, b, p.lds, st, a);
             else hipLaunchKernelGGL((k_layout1s<ELEM, MODE, XBF16, 4, false>), g, b, p.lds, st, a);
