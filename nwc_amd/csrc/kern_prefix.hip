@@ -186,13 +186,17 @@ __device__ __forceinline__ float row0(Seq<ELEM, STRIDE> &S, const LutLds &s, con
     return sum;
 }
 
-// Rows r0 .. r0 + NR - 1 of one layout-0 block for one lane, decoded from LDS starting at bit position P0 of the lane's
-// stream, with the first four of those raw-plane rows already requested into `ring`.  Returns the row sums reduced over the half-wave (NR = 8: lane
-// 4r holds row r0 + r; NR = 4: lane 8r) or, for dequantization, stores the rows; MODE kRowIndex records the row
+// Rows r0 .. r0 + NR - 1 of one layout-0 block for one lane, decoded from LDS starting at bit position P0 of the
+// lane's stream, with the first kRing0 of those raw-plane rows already requested into `ring`.  Returns the row sums
+// reduced over the half-wave (NR = 8: lane 4r holds row r0 + r; NR = 4: lane 8r) or, for dequantization, stores the rows; MODE kRowIndex records the row
 // index (positions of rows 2, 4, 6) instead.  Fully unrolled: every row's raw bytes live in their own registers.
+// Raw rows in flight per half-wave: two.  The prologue then requests the streams and only rows 0-1, so decoding
+// starts sooner; each later row has one row's decode time to arrive (a deeper ring, or rows requested before the
+// streams, measured slower: the whole chip's first requests compete for HBM).
+constexpr int kRing0 = 2;
 template <int ELEM, int MODE, bool XBF16, int NR>
 __device__ __forceinline__ float rowsN(const LutLds &s, const uint32_t *lane, uint32_t P0, const BlockArgs &a, const Shape &f,
-                                       const XRegs<XBF16> &x, uint4 ring[4], const Coord0 &c, uint32_t r0, uint32_t L) {
+                                       const XRegs<XBF16> &x, uint4 ring[kRing0], const Coord0 &c, uint32_t r0, uint32_t L) {
     Seq<ELEM> S;
     S.init_at(lane, P0);
     float acc[NR];
@@ -201,9 +205,9 @@ __device__ __forceinline__ float rowsN(const LutLds &s, const uint32_t *lane, ui
         if (MODE == kRowIndex && r > 0 && (r & 1) == 0)
             ((uint16_t *)a.out)[((uint64_t)c.b * kRowIndexSplits + (r >> 1) - 1) * kLanes + L] = (uint16_t)S.position(lane);
         uint32_t pw[8];
-        const float sum = row0<ELEM, MODE, XBF16>(S, s, ring[r & 3], x, pw);
-        // eight rows go through a ring of four registers: row r + 4 is requested when row r is done
-        if (MODE != kRowIndex && r + 4 < NR) ring[r & 3] = raw_row<ELEM>(a.low, f, c, r0 + r + 4);
+        const float sum = row0<ELEM, MODE, XBF16>(S, s, ring[r % kRing0], x, pw);
+        // eight rows go through a ring of kRing0 registers: row r + kRing0 is requested when row r is done
+        if (MODE != kRowIndex && r + kRing0 < NR) ring[r % kRing0] = raw_row<ELEM>(a.low, f, c, r0 + r + kRing0);
         if (MODE == kDequant) store_row0<MODE>(a, f, c.row0 + r0 + r, c.col0, c.col_ok, pw);
         else acc[r] = c.col_ok ? sum : 0.f;
     }
@@ -327,12 +331,12 @@ __global__ void __launch_bounds__(1024) k_layout0(BlockArgs a) {
     const uint32_t mend = B0 + nt == nb ? matrix_end(a, nb) : 0u;
     // request order: region bounds and table first, then the stream copy (which needs the bounds), then the raw rows
     // and activations; loads complete in order, so each wait below covers only what it needs
-    Region R = region_of(a, B0, B0 + min(HB, nt), nb, mend);
-    LutLoad Q;
-    lut_issue(Q, a.lut);
     uint32_t t = hw / SP;
     const uint32_t r0 = (hw % SP) * NR;                       // first row of this half-wave's share of the block
     Coord0 c = coord0(min(t, tl), rg0, f, L);
+    Region R = region_of(a, B0, B0 + min(HB, nt), nb, mend);
+    LutLoad Q;
+    lut_issue(Q, a.lut);
     uint32_t n = a.hdr[(uint64_t)c.b * kHdrBytes + L], base = a.bases[c.b];
     const uint32_t P0 = r0 ? a.aux[((uint64_t)c.b * kRowIndexSplits + (r0 >> 1) - 1) * kLanes + L] : 0u;
     Bulk Bk;
@@ -343,9 +347,9 @@ __global__ void __launch_bounds__(1024) k_layout0(BlockArgs a) {
     if constexpr (!PIPE) {
         // the table is stored before the raw rows are requested, so its registers are free for them
         lut_commit<kLutSeq>(s, Q, a.lut);
-        uint4 raw[4];
+        uint4 raw[kRing0];
 #pragma unroll
-        for (int r = 0; r < (NR < 4 ? NR : 4); r++)
+        for (int r = 0; r < (NR < kRing0 ? NR : kRing0); r++)
             raw[r] = MODE == kRowIndex ? make_uint4(0u, 0u, 0u, 0u) : raw_row<ELEM>(a.low, f, c, r0 + r);
         const bool fits = R.n16 * 4u <= cap;
         if (fits) bulk_commit(Bk, cur, R, tid, nth);
@@ -513,8 +517,7 @@ __global__ void __launch_bounds__(1024) k_layout1(BlockArgs a) {
 // Layout 1, single round: a workgroup owns G whole 16-row groups (nt = G * CB <= H / SP blocks); their streams are
 // staged once into LDS like layout 0's, and each half-wave decodes super-chunks sc0 .. sc0 + NS - 1 of one block
 // (SP = 16 / NS half-waves per block; with SP > 1 the row index gives each lane's bit position at super-chunk
-// 4, 8, 12).  Raw super-chunks go through a ring of four registers (chunk s + 4 is requested when chunk s is done),
-// activations one super-chunk ahead.  Partial row sums are kept per (row, column block, part) and summed in a fixed
+// 4, 8, 12).  Raw super-chunks go through a ring of two registers (chunk s + 2 is requested when chunk s is done).  Partial row sums are kept per (row, column block, part) and summed in a fixed
 // order by the workgroup.
 struct Coord1 {
     uint32_t g, cb, b, rb, nsc;
@@ -559,12 +562,15 @@ __device__ __forceinline__ void stage_x1(uint4 *xs, const void *x, uint32_t n8, 
     for (uint32_t i = tid + 2u * nth; i < n8; i += nth) xs[i] = x8_at<XBF16>(x, 8u * i);
 }
 
+// Raw super-chunks in flight per half-wave in the single-round kernel: two, as for layout 0's rows.
+constexpr int kRing1 = 2;
 // NEXT (NS = 4, several items per half-wave): each ring slot is refilled with the next item's super-chunk once used.
 template <int ELEM, int MODE, int NS, bool FULL, bool NEXT = false>
 __device__ __forceinline__ float2 chunks1(const LutLds &s, const uint32_t *lane, uint32_t P0, const BlockArgs &a,
                                           const Shape &f, const uint4 *xs, uint4 ring[4], const Coord1 &c, uint32_t sc0,
                                           uint32_t L, const Coord1 *cn = nullptr, uint32_t nsc0 = 0) {
     static_assert(!NEXT || NS == 4, "next-item refills for four-super-chunk items");
+    constexpr int D = NEXT ? 4 : kRing1;                        // raw super-chunks in flight
     const uint32_t r = L >> 2, q = L & 3;
     Seq<ELEM> S;
     S.init_at(lane, P0);
@@ -578,7 +584,7 @@ __device__ __forceinline__ float2 chunks1(const LutLds &s, const uint32_t *lane,
             ((uint16_t *)a.out)[((uint64_t)c.b * kRowIndexSplits + (i >> 2) - 1) * kLanes + L] = (uint16_t)S.position(lane);
         uint4 xc = make_uint4(0u, 0u, 0u, 0u);
         if (MODE == kToken || MODE == kF32) xc = xs[(kc0 + sc * 32u) >> 3];
-        const uint4 cw = ring[i & 3];
+        const uint4 cw = ring[i % D];
         uint32_t pa[4], pb[4];
 #pragma unroll
         for (int k = 0; k < 4; k++) {
@@ -603,8 +609,8 @@ __device__ __forceinline__ float2 chunks1(const LutLds &s, const uint32_t *lane,
                 asm volatile("" : "+v"(accA), "+v"(accB));
             }
         }
-        if constexpr (NEXT) ring[i & 3] = raw1<ELEM>(a.low, *cn, nsc0 + i);
-        else if (MODE != kRowIndex && i + 4 < NS) ring[i & 3] = raw1<ELEM>(a.low, c, sc + 4u);
+        if constexpr (NEXT) ring[i % D] = raw1<ELEM>(a.low, *cn, nsc0 + i);
+        else if (MODE != kRowIndex && i + D < NS) ring[i % D] = raw1<ELEM>(a.low, c, sc + (uint32_t)D);
         if (MODE == kDequant) {
             const uint32_t kc = kc0 + sc * 32u, row0 = c.rb * kRows12;
             if (kc < f.K16) {                                   // a half super-chunk beyond K16 is filler
@@ -700,7 +706,7 @@ __global__ void __launch_bounds__(1024) k_layout1s(BlockArgs a) {
     lut_commit<kLutSeq>(s, Q, a.lut);
     uint4 ring[4];
 #pragma unroll
-    for (int i = 0; i < 4; i++) ring[i] = MODE == kRowIndex ? make_uint4(0u, 0u, 0u, 0u) : raw1<ELEM>(a.low, c, sc0 + i);
+    for (int i = 0; i < kRing1; i++) ring[i] = MODE == kRowIndex ? make_uint4(0u, 0u, 0u, 0u) : raw1<ELEM>(a.low, c, sc0 + i);
     // the copy moves four 16-byte chunks per thread (512 words per half-wave); a larger region (one half-wave per
     // block, as when the row index is built) decodes from global memory
     const bool fits = R.n16 <= 4u * nth && R.n16 * 4u <= cap;

@@ -238,16 +238,17 @@ def test_row_index_values(cuda, M, K, escapes):
 
 @pytest.mark.parametrize("layout,M,K,split,escapes", [
     (0, 2560, 4096, 4, "none"), (0, 6144, 2560, 2, "none"), (0, 1003, 1100, 4, "none"), (0, 2560, 4096, 4, "sparse"),
-    (0, 2560, 4096, 4, "dense"), (0, 6144, 2560, 2, "dense"), (0, 1003, 1100, 4, "dense"),
+    (0, 2560, 4096, 4, "dense"), (0, 6144, 2560, 2, "dense"), (0, 1003, 1100, 4, "dense"), (0, 2560, 4096, 4, "heavy"),
+    (0, 6144, 2560, 2, "heavy"),
     (1, 2560, 4096, 4, "none"), (1, 6144, 2560, 4, "none"), (1, 19456, 2560, 2, "none"), (1, 1003, 1100, 4, "none"),
     (1, 2560, 4096, 4, "dense"), (1, 1003, 1100, 4, "dense"),
-    (1, 2560, 9728, 4, "none"), (1, 2560, 9728, 4, "dense"), (1, 1003, 9000, 4, "none")])
+    (1, 2560, 9728, 4, "none"), (1, 2560, 9728, 4, "dense"), (1, 1003, 9000, 4, "none"), (1, 2560, 4096, 4, "heavy"),
+    (1, 2560, 9728, 4, "heavy")])
 def test_token_path_with_and_without_row_index(cuda, layout, M, K, split, escapes):
     """The split decode (layout 0: four or two half-waves per block, each reducing 2 or 4 rows; layout 1: super-chunk
-    ranges 4 or 8 long, and for K > 8192 several such items per half-wave) against the whole-block decode: o_proj,
-    qkv_proj, gate_up and down shapes on 256 CUs, ragged matrices (layout 1: a last column block of three or two
-    super-chunks), and escape runs (24-bit codes) dense enough that tiles do not fit their LDS region and decode from
-    global memory."""
+    ranges 4 or 8 long, and for K > 8192 several such items per half-wave) against the whole-block decode: o_proj, qkv_proj, gate_up and down shapes on 256 CUs,
+    ragged matrices (layout 1: a last column block of three or two super-chunks), and escape runs (24-bit codes) dense
+    enough ("heavy": three whole row groups) that tiles do not fit their LDS region and decode from global memory."""
     from nwc_amd.nwc_torch import _lib, _ptr, _stream
     NWCWeight, _, _ = _nwc()
     w = bf16_matrix(M, K, seed=77, escapes=escapes == "sparse")
@@ -257,6 +258,9 @@ def test_token_path_with_and_without_row_index(cuda, layout, M, K, split, escape
         w[9, 512:700] = -big
         w[13, 1024:1100] = big
         w[16:24, 16:32] = -big
+    if escapes == "heavy":                    # rows 0-23 all escapes: the first workgroups' streams exceed their region
+        sign = torch.randint(0, 2, (24, K), generator=torch.Generator().manual_seed(5)) * 2 - 1
+        w[0:24] = (sign * 1e30).to(torch.bfloat16)
     c = NWCWeight(w, device="cuda", layout=layout)
     assert _lib.nwc_token_split(c.n, K, c.code, 1) == split
     assert _lib.nwc_token_split(c.n, K, c.code, 0) == 1
