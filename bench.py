@@ -79,9 +79,9 @@ class Launch:
     def __init__(self, c, x, y):
         from nwc_amd.nwc_torch import _lib, _ptr
         self.fn = _lib.nwc_linear_xbf16
-        ri = c.row_index()
+        ri, st = c.row_index(), c.seq_table()
         self.args = [_ptr(c.data), _ptr(c.bases), _ptr(c.hdr), _ptr(c.lut), _ptr(c.low),
-                     _ptr(ri) if ri is not None else None, _ptr(x), None,
+                     _ptr(ri) if ri is not None else None, _ptr(st) if st is not None else None, _ptr(x), None,
                      _ptr(c.scale) if c.scale is not None else None, _ptr(y), ctypes.c_uint64(c.n),
                      ctypes.c_uint32(c.in_features), ctypes.c_int(c.code)]
 

@@ -49,7 +49,20 @@ constexpr uint32_t kDynLdsPipe = 62u * 1024u;         // two such workgroups per
 // that does not fit decodes from global memory), so 32 blocks fit two workgroups per CU.
 constexpr uint32_t kSlotWords2 = 440;
 
-bool plan_layout0(const Shape &f, int mode, int ncu, bool index, LaunchPlan &p) {
+// With the 13-bit decode table (32 KB of static LDS instead of 16 KB) two workgroups still share a CU's 160 KB when
+// their dynamic LDS stays under this; the single-round tiers are tried with it first.
+constexpr uint32_t kDynLds13 = 47u * 1024u;
+
+bool plan_layout0_tiers(const Shape &f, int mode, int ncu, bool index, uint32_t budget, bool single_only, LaunchPlan &p);
+bool plan_layout0(const Shape &f, int mode, int ncu, bool index, bool seq, LaunchPlan &p) {
+    if (seq && mode == kToken && plan_layout0_tiers(f, mode, ncu, index, kDynLds13, true, p)) {
+        p.seq13 = true;
+        return true;
+    }
+    return plan_layout0_tiers(f, mode, ncu, index, kDynLdsPipe, false, p);
+}
+
+bool plan_layout0_tiers(const Shape &f, int mode, int ncu, bool index, uint32_t budget, bool single_only, LaunchPlan &p) {
     p = LaunchPlan{};
     p.layout = 0;
     const bool rows = mode == kToken || mode == kF32;
@@ -71,7 +84,7 @@ bool plan_layout0(const Shape &f, int mode, int ncu, bool index, LaunchPlan &p) 
     if (index && rows) {
         const uint32_t G = std::max(1u, ceil_div(groups, 2u * ncu_)), blocks = G * CB;
         const uint32_t lds = blocks * kSlotWords0 * 4u + G * part;
-        if (lds <= kDynLdsPipe) {
+        if (lds <= budget) {
             if (4u * blocks <= 32u) return set(false, 4u, G, 4u * blocks, kSlotWords0, lds);
             if (2u * blocks <= 20u) return set(false, 2u, G, 2u * blocks, kSlotWords0, lds);
         }
@@ -82,8 +95,9 @@ bool plan_layout0(const Shape &f, int mode, int ncu, bool index, LaunchPlan &p) 
         const uint32_t G = std::max(1u, ceil_div(groups, 2u * ncu_)), blocks = G * CB;
         const uint32_t halves = (blocks + 1u) & ~1u;
         const uint32_t lds = halves * kSlotWords2 * 4u + G * part;
-        if (blocks <= 32u && lds <= kDynLdsPipe) return set(false, 1u, G, halves, kSlotWords2, lds);
+        if (blocks <= 32u && lds <= budget) return set(false, 1u, G, halves, kSlotWords2, lds);
     }
+    if (single_only) return false;
     // 3. several blocks per half-wave: rounds through two region buffers, two workgroups per CU
     uint32_t G = std::max(1u, ceil_div(groups, 2u * ncu_));
     for (;; G--) {
@@ -154,8 +168,8 @@ bool plan_layout1(const Shape &f, int mode, int ncu, bool index, LaunchPlan &p) 
 // Layouts 1/2: workgroup tile = G whole row groups, one block per half-wave where the LDS budget allows.  Prefer at
 // least two workgroups per CU (small matrices spread over the whole chip), at most 32 blocks (16 waves) per
 // workgroup, and an even block count so both halves of every wave have a block.
-bool plan_blocks(const Shape &f, int layout, int mode, int ncu, bool index, LaunchPlan &p) {
-    if (layout == 0) return plan_layout0(f, mode, ncu, index, p);
+bool plan_blocks(const Shape &f, int layout, int mode, int ncu, bool index, LaunchPlan &p, bool seq = false) {
+    if (layout == 0) return plan_layout0(f, mode, ncu, index, seq, p);
     if (layout == 1 && plan_layout1(f, mode, ncu, index, p)) return true;
     if (mode == kRowIndex) return false;
     p = LaunchPlan{};
@@ -185,15 +199,15 @@ bool plan_blocks(const Shape &f, int layout, int mode, int ncu, bool index, Laun
 
 int run_blocks(int mode, bool xbf16, hipStream_t st, const uint8_t *data, const uint32_t *bases, const uint8_t *hdr,
                const uint32_t *tab, const uint8_t *low, const void *x, const uint16_t *bias, const float *scale, void *out,
-               uint64_t n, uint32_t K, int elem, const uint16_t *aux = nullptr) {
+               uint64_t n, uint32_t K, int elem, const uint16_t *aux = nullptr, const uint32_t *seq = nullptr) {
     const int ncu = current_cus();
     if (ncu <= 0) return (int)hipErrorNoDevice;
     const int layout = elem_layout(elem), t = elem_type(elem);
     const Shape f((uint32_t)(n / K), K, layout);
     LaunchPlan p;
-    if (!plan_blocks(f, layout, mode, ncu, aux != nullptr && layout <= 1, p)) return -1;
+    if (!plan_blocks(f, layout, mode, ncu, aux != nullptr && layout <= 1, p, seq != nullptr && layout == 0 && xbf16)) return -1;
     BlockArgs a{data, bases, hdr, tab, low, x, bias, scale, out, aux, f.M, f.K, p.G,
-                layout == 0 || p.split ? p.slot_words : slot_words_for(layout)};
+                layout == 0 || p.split ? p.slot_words : slot_words_for(layout), seq};
     return layout == 2 ? launch_fixed(p, t, mode, xbf16, a, st) : launch_prefix(p, t, mode, xbf16, a, st);
 }
 
@@ -223,11 +237,11 @@ extern "C" int nwc_linear_bf16(void *stream, const uint8_t *data, const uint32_t
 }
 
 extern "C" int nwc_linear_xbf16(void *stream, const uint8_t *data, const uint32_t *bases, const uint8_t *hdr, const uint32_t *tab,
-                                const uint8_t *low, const uint16_t *row_index, const uint16_t *x, const uint16_t *bias,
-                                const float *scale, uint16_t *y, uint64_t n, uint32_t K, int elem) {
+                                const uint8_t *low, const uint16_t *row_index, const uint32_t *seq_table, const uint16_t *x,
+                                const uint16_t *bias, const float *scale, uint16_t *y, uint64_t n, uint32_t K, int elem) {
     if (!shape_ok(n, kBlock, K, elem)) return -1;
     return run_blocks(kToken, true, (hipStream_t)stream, data, bases, hdr, tab, low, x, bias, scale, y, n, K, elem,
-                      elem_layout(elem) <= 1 ? row_index : nullptr);
+                      elem_layout(elem) <= 1 ? row_index : nullptr, elem_layout(elem) == 0 ? seq_table : nullptr);
 }
 
 extern "C" int nwc_row_index(void *stream, const uint8_t *data, const uint32_t *bases, const uint8_t *hdr, const uint32_t *tab,

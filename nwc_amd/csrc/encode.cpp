@@ -447,3 +447,36 @@ extern "C" void nwc_build_tab(const uint16_t *freq, const uint16_t *psym, int el
     lut[0] = kFlag | (uint32_t)(psym[11] & 0x7F) << 8 | (uint32_t)(psym[12] & 0x7F) << 16;
     lut[1] = kFlag | (uint32_t)(psym[13] & 0x7F) << 8 | (uint32_t)(psym[14] & 0x7F) << 16;
 }
+
+// Token-path decode table of layout 0 with a 13-bit window, built from a stored LUT (its exp_of_rank): for every
+// 13-bit window that starts with two complete codes, (17 - c) | b0 << 8 | b1 << 16, the step encoding of the gfx950
+// kernel (byte 0 is the right shift that brings the second pair's 13 bits to [14:2]); for every other window the slow
+// marker 0x40000000.  out[8192..8195] hold exp_of_rank[0..15] (the slow path's rank -> byte map).  Not part of the
+// format: a 13-bit window makes a pair too long for the table 3-4x rarer than the stored 12-bit LUT does (0.025%
+// instead of 0.087% of code pairs for N(0, 0.02^2) BF16), and each such pair costs its wave a code-by-code redo.
+extern "C" int nwc_seq_table(const uint32_t *lut, int elem, uint32_t *out) {
+    if (elem_layout(elem) > 1) return -1;
+    const uint32_t maxr = elem_type(elem) == kElemFp8 ? kMaxRankFp8 : kMaxRankBf16;
+    uint8_t eor[16] = {0};
+    for (uint32_t q = 0; q < 15; q++) {                            // where lut_issue finds them (nwc_device.h)
+        const uint32_t w = lut[q < 11u ? (1u << (kPeek - 1u - q)) : (q - 11u) >> 1];
+        eor[q] = (uint8_t)((w >> ((q < 11u || (q & 1u)) ? 8u : 16u)) & 0x7Fu);
+    }
+    constexpr uint32_t P = kPeekSeq;
+    for (uint32_t pat = 0; pat < (1u << P); pat++) {
+        uint32_t start = 0, got = 0, bytes[2] = {0, 0};
+        while (got < 2) {
+            uint32_t z = 0;
+            while (start + z < P && !((pat >> (P - 1 - start - z)) & 1)) z++;
+            if (z >= maxr || start + z + 2 > P) break;
+            const uint32_t sign = (pat >> (P - 1 - (start + z + 1))) & 1;
+            bytes[got++] = (sign << 7) | eor[z];
+            start += z + 2;
+        }
+        out[pat] = got == 2 ? (30u - P - start) | bytes[0] << 8 | bytes[1] << 16 : 0x40000000u;
+    }
+    for (uint32_t j = 0; j < 4; j++)
+        out[(1u << P) + j] = eor[4 * j] | (uint32_t)eor[4 * j + 1] << 8 | (uint32_t)eor[4 * j + 2] << 16 |
+                             (uint32_t)eor[4 * j + 3] << 24;
+    return 0;
+}

@@ -162,8 +162,8 @@ __device__ __forceinline__ void bulk_commit(const Bulk &B, uint32_t *buf, const 
 // activations or, for dequantization, the eight BF16 pairs in pw.  A step whose table entries were not both fast in
 // some lane of the wave is redone code by code from its start by the whole wave (0.09% of lane-steps, 5% of
 // wave-steps for N(0, 0.02^2) BF16 at a 12-bit window).
-template <int ELEM, int MODE, bool XBF16, int STRIDE = 1>
-__device__ __forceinline__ float row0(Seq<ELEM, STRIDE> &S, const LutLds &s, const uint4 &rw, const XRegs<XBF16> &x,
+template <int ELEM, int MODE, bool XBF16, int STRIDE = 1, class Tab>
+__device__ __forceinline__ float row0(Seq<ELEM, STRIDE> &S, const Tab &s, const uint4 &rw, const XRegs<XBF16> &x,
                                       uint32_t pw[8]) {
     float sum = 0.f;
 #pragma unroll
@@ -186,16 +186,18 @@ __device__ __forceinline__ float row0(Seq<ELEM, STRIDE> &S, const LutLds &s, con
     return sum;
 }
 
-// Rows r0 .. r0 + NR - 1 of one layout-0 block for one lane, decoded from LDS starting at bit position P0 of the
-// lane's stream, with the first kRing0 of those raw-plane rows already requested into `ring`.  Returns the row sums
-// reduced over the half-wave (NR = 8: lane 4r holds row r0 + r; NR = 4: lane 8r) or, for dequantization, stores the rows; MODE kRowIndex records the row
-// index (positions of rows 2, 4, 6) instead.  Fully unrolled: every row's raw bytes live in their own registers.
 // Raw rows in flight per half-wave: two.  The prologue then requests the streams and only rows 0-1, so decoding
 // starts sooner; each later row has one row's decode time to arrive (a deeper ring, or rows requested before the
 // streams, measured slower: the whole chip's first requests compete for HBM).
 constexpr int kRing0 = 2;
-template <int ELEM, int MODE, bool XBF16, int NR>
-__device__ __forceinline__ float rowsN(const LutLds &s, const uint32_t *lane, uint32_t P0, const BlockArgs &a, const Shape &f,
+
+// Rows r0 .. r0 + NR - 1 of one layout-0 block for one lane, decoded from LDS starting at bit position P0 of the
+// lane's stream, with the first kRing0 of those raw-plane rows already requested into `ring`.  Returns the row sums
+// reduced over the half-wave (NR = 8: lane 4r holds row r0 + r; NR = 4: lane 8r) or, for dequantization, stores the
+// rows; MODE kRowIndex records the row index (positions of rows 2, 4, 6) instead.  Fully unrolled: every row's raw
+// bytes live in their own registers.
+template <int ELEM, int MODE, bool XBF16, int NR, class Tab>
+__device__ __forceinline__ float rowsN(const Tab &s, const uint32_t *lane, uint32_t P0, const BlockArgs &a, const Shape &f,
                                        const XRegs<XBF16> &x, uint4 ring[kRing0], const Coord0 &c, uint32_t r0, uint32_t L) {
     Seq<ELEM> S;
     S.init_at(lane, P0);
@@ -251,8 +253,8 @@ __device__ __forceinline__ float rows0_ring(const LutLds &s, const uint32_t *wor
 // with a rolled row loop and its own raw loads (compact code; such rounds are rare, e.g. near-uniform exponent
 // distributions).  Lanes past K16 have empty streams; the callers point them at the block's first word: decoding zero
 // bits walks at most 96 words (all escapes), less than one block of such a round.
-template <int ELEM, int MODE, bool XBF16>
-__device__ __forceinline__ float rows0_global(const LutLds &s, const uint32_t *words, const BlockArgs &a, const Shape &f,
+template <int ELEM, int MODE, bool XBF16, class Tab>
+__device__ __forceinline__ float rows0_global(const Tab &s, const uint32_t *words, const BlockArgs &a, const Shape &f,
                                               const XRegs<XBF16> &x, const Coord0 &c, bool valid, uint32_t L) {
     Seq<ELEM> S;
     S.init(words);
@@ -276,8 +278,8 @@ __device__ __forceinline__ float rows0_global(const LutLds &s, const uint32_t *w
 }
 
 // rowsN for a half-wave share of a block whose round does not fit the region buffer: from global memory, rolled.
-template <int ELEM, int MODE, bool XBF16, int NR>
-__device__ __forceinline__ float rowsN_global(const LutLds &s, const uint32_t *lane, uint32_t P0, const BlockArgs &a,
+template <int ELEM, int MODE, bool XBF16, int NR, class Tab>
+__device__ __forceinline__ float rowsN_global(const Tab &s, const uint32_t *lane, uint32_t P0, const BlockArgs &a,
                                               const Shape &f, const XRegs<XBF16> &x, const Coord0 &c, uint32_t r0, uint32_t L) {
     Seq<ELEM> S;
     S.init_at(lane, P0);
@@ -310,12 +312,26 @@ __device__ __forceinline__ float rowsN_global(const LutLds &s, const uint32_t *l
 //   PIPE = true: two region buffers; while round k decodes, round k + 1's streams, raw rows (four-register ring) and
 //     activations are in flight and round k + 2's bounds and header bytes are read, so after the first round no step
 //     waits on global memory.  One barrier per round publishes the next region.
-template <int ELEM, int MODE, bool XBF16, bool PIPE, int NR>
+// Staging of the decode table: the stored 12-bit LUT, re-encoded (PEEK 12), or the prepared 13-bit table (PEEK 13).
+template <int PEEK> struct TabStage;
+template <> struct TabStage<kPeek> {
+    LutLoad Q;
+    __device__ __forceinline__ void issue(const BlockArgs &a) { lut_issue(Q, a.lut); }
+    __device__ __forceinline__ void commit(LutLds &s, const BlockArgs &a) { lut_commit<kLutSeq>(s, Q, a.lut); }
+};
+template <> struct TabStage<kPeekSeq> {
+    SeqLoad Q;
+    __device__ __forceinline__ void issue(const BlockArgs &a) { seq_issue(Q, a.seq); }
+    __device__ __forceinline__ void commit(LutLds13 &s, const BlockArgs &a) { seq_commit(s, Q, a.seq); }
+};
+
+template <int ELEM, int MODE, bool XBF16, bool PIPE, int NR, int PEEK = kPeek>
 __global__ void __launch_bounds__(1024) k_layout0(BlockArgs a) {
     static_assert(NR == 8 || ((NR == 4 || NR == 2) && !PIPE), "row splits only in the single-round kernel");
+    static_assert(PEEK == kPeek || !PIPE, "the 13-bit table only in the single-round kernel");
     constexpr uint32_t SP = kRows0 / NR;                      // half-waves per block
     constexpr bool ROWS = MODE == kToken || MODE == kF32;     // modes that keep row sums
-    __shared__ LutLds s;
+    __shared__ LutT<PEEK> s;
     extern __shared__ uint32_t dyn[];
     const uint32_t tid = threadIdx.x, nth = blockDim.x, L = tid & 31;
     const uint32_t hw = tid >> 5, H = nth >> 5;
@@ -335,8 +351,8 @@ __global__ void __launch_bounds__(1024) k_layout0(BlockArgs a) {
     const uint32_t r0 = (hw % SP) * NR;                       // first row of this half-wave's share of the block
     Coord0 c = coord0(min(t, tl), rg0, f, L);
     Region R = region_of(a, B0, B0 + min(HB, nt), nb, mend);
-    LutLoad Q;
-    lut_issue(Q, a.lut);
+    TabStage<PEEK> Q;
+    Q.issue(a);
     uint32_t n = a.hdr[(uint64_t)c.b * kHdrBytes + L], base = a.bases[c.b];
     const uint32_t P0 = r0 ? a.aux[((uint64_t)c.b * kRowIndexSplits + (r0 >> 1) - 1) * kLanes + L] : 0u;
     Bulk Bk;
@@ -346,7 +362,7 @@ __global__ void __launch_bounds__(1024) k_layout0(BlockArgs a) {
 
     if constexpr (!PIPE) {
         // the table is stored before the raw rows are requested, so its registers are free for them
-        lut_commit<kLutSeq>(s, Q, a.lut);
+        Q.commit(s, a);
         uint4 raw[kRing0];
 #pragma unroll
         for (int r = 0; r < (NR < kRing0 ? NR : kRing0); r++)
@@ -371,7 +387,7 @@ __global__ void __launch_bounds__(1024) k_layout0(BlockArgs a) {
         Coord0 cn = coord0(min(t + H, tl), rg0, f, L);
         uint32_t n_n = a.hdr[(uint64_t)cn.b * kHdrBytes + L], base_n = a.bases[cn.b];
         Region Rn = region_of(a, B0 + min(H, tl), B0 + min(2u * H, nt), nb, mend);
-        lut_commit<kLutSeq>(s, Q, a.lut);
+        Q.commit(s, a);
         if (R.n16 * 4u <= cap) bulk_commit(Bk, cur, R, tid, nth);
         __syncthreads();
         const uint32_t rounds = (nt + H - 1u) / H;
@@ -964,7 +980,18 @@ template <int ELEM, int MODE, bool XBF16>
 static int launch_prefix_t(const LaunchPlan &p, const BlockArgs &a, hipStream_t st) {
     if (p.layout == 0 && p.pipe)
         hipLaunchKernelGGL((k_layout0<ELEM, MODE, XBF16, true, 8>), dim3(p.grid), dim3(p.threads), p.lds, st, a);
-    else if (p.layout == 0 && p.split == 2 && (MODE == kToken || MODE == kF32))
+    if constexpr (MODE == kToken && XBF16) {
+        if (p.layout == 0 && p.seq13 && !p.pipe) {
+            if (p.split == 2)
+                hipLaunchKernelGGL((k_layout0<ELEM, MODE, XBF16, false, 4, kPeekSeq>), dim3(p.grid), dim3(p.threads), p.lds, st, a);
+            else if (p.split == 4)
+                hipLaunchKernelGGL((k_layout0<ELEM, MODE, XBF16, false, 2, kPeekSeq>), dim3(p.grid), dim3(p.threads), p.lds, st, a);
+            else
+                hipLaunchKernelGGL((k_layout0<ELEM, MODE, XBF16, false, 8, kPeekSeq>), dim3(p.grid), dim3(p.threads), p.lds, st, a);
+            return (int)hipGetLastError();
+        }
+    }
+    if (p.layout == 0 && p.split == 2 && (MODE == kToken || MODE == kF32))
         hipLaunchKernelGGL((k_layout0<ELEM, MODE, XBF16, false, 4>), dim3(p.grid), dim3(p.threads), p.lds, st, a);
     else if (p.layout == 0 && p.split == 4 && (MODE == kToken || MODE == kF32))
         hipLaunchKernelGGL((k_layout0<ELEM, MODE, XBF16, false, 2>), dim3(p.grid), dim3(p.threads), p.lds, st, a);

@@ -127,10 +127,12 @@ __device__ __forceinline__ float reduce2_transposed(float acc[2], uint32_t L) {
 enum LutKind { kLutWindow = 0, kLutSeq = 1 };
 constexpr uint32_t kSeqSlow = 0x40000000u, kSeqSlowTest = 0x20000000u;
 
-struct LutLds {
-    uint32_t tab[kLutWords];
-    uint8_t eor[16];            // exp_of_rank, read back from the table (the slow path's rank -> byte map)
+template <int PEEK> struct LutT {
+    uint32_t tab[1u << PEEK];
+    alignas(16) uint8_t eor[16];    // exp_of_rank, read back from the table (the slow path's rank -> byte map)
 };
+using LutLds = LutT<kPeek>;
+using LutLds13 = LutT<kPeekSeq>;
 
 template <int KIND>
 __device__ __forceinline__ uint32_t lut_transform(uint32_t e) {
@@ -185,8 +187,36 @@ __device__ __forceinline__ void stage_lut(LutLds &s, const uint32_t *__restrict_
     __syncthreads();
 }
 
-__device__ __forceinline__ uint32_t lds_entry(const LutLds &s, uint32_t byte_off) {
+template <int PEEK>
+__device__ __forceinline__ uint32_t lds_entry(const LutT<PEEK> &s, uint32_t byte_off) {
     return *(const uint32_t *)((const char *)s.tab + byte_off);
+}
+
+// The 13-bit table (nwc_seq_table: entries already encoded, exp_of_rank in the last four words) copied into LDS:
+// three 16-byte chunks per thread for >= 683 threads, then the rest; the caller publishes it with a barrier.
+struct SeqLoad {
+    u32x4_t v0, v1, v2;
+};
+__device__ __forceinline__ void seq_issue(SeqLoad &Q, const uint32_t *__restrict__ tab) {
+    const uint32_t tid = threadIdx.x, nth = blockDim.x;
+    constexpr uint32_t n4 = kSeqTableWords / 4;
+    const u32x4_t *t4 = (const u32x4_t *)tab;
+    Q.v0 = t4[min(tid, n4 - 1u)];
+    Q.v1 = t4[min(tid + nth, n4 - 1u)];
+    Q.v2 = t4[min(tid + 2u * nth, n4 - 1u)];
+}
+__device__ __forceinline__ void seq_store(LutLds13 &s, uint32_t i, u32x4_t v) {
+    constexpr uint32_t n4 = kSeqTableWords / 4;
+    if (i < n4 - 1u) ((u32x4_t *)s.tab)[i] = v;
+    else if (i == n4 - 1u) *(u32x4_t *)s.eor = v;                      // the last chunk: exp_of_rank
+}
+__device__ __forceinline__ void seq_commit(LutLds13 &s, const SeqLoad &Q, const uint32_t *__restrict__ tab) {
+    const uint32_t tid = threadIdx.x, nth = blockDim.x;
+    constexpr uint32_t n4 = kSeqTableWords / 4;
+    seq_store(s, tid, Q.v0);
+    seq_store(s, tid + nth, Q.v1);
+    seq_store(s, tid + 2u * nth, Q.v2);
+    for (uint32_t i = tid + 3u * nth; i < n4; i += nth) seq_store(s, i, ((const u32x4_t *)tab)[i]);   // < 683 threads
 }
 
 // ---- prefix-code window ----
@@ -319,17 +349,21 @@ struct Seq {
     // those of weights 2,3.  Byte 0 of e1 + e2 is 36 - c (kLutSeq), so t = e1 + e2 + s - 36 has s - c in its low byte
     // (bytes 1-3 hold exponent sums and do not matter).  Returns t: the step is correct only if t < kSeqSlowTest;
     // otherwise the caller resets the position and redoes the step with slow_quad.
-    __device__ __forceinline__ uint32_t fast_quad(const LutLds &T, uint32_t &e1, uint32_t &e2) {
+    // With a PEEK-bit table (12: the stored LUT re-encoded; 13: nwc_seq_table) byte 0 of an entry is 30 - PEEK - c.
+    template <int PEEK>
+    __device__ __forceinline__ uint32_t fast_quad(const LutT<PEEK> &T, uint32_t &e1, uint32_t &e2) {
+        constexpr uint32_t mask = ((1u << PEEK) - 1u) << 2;
         const uint32_t hi = window();
-        e1 = lds_entry(T, (hi >> 18) & 0x3FFCu);
-        e2 = lds_entry(T, (hi >> (e1 & 31u)) & 0x3FFCu);               // the 12 bits after the first c1
-        const uint32_t t = e1 + e2 + (s - 36u);
+        e1 = lds_entry(T, (hi >> (30 - PEEK)) & mask);
+        e2 = lds_entry(T, (hi >> (e1 & 31u)) & mask);                  // the PEEK bits after the first c1
+        const uint32_t t = e1 + e2 + (s - 2u * (30u - PEEK));
         step(t);
         return t;
     }
 
     // one code by counting leading zeros: rank r < max -> r zeros, one, sign; BF16 escape -> 15 zeros, one, byte
-    __device__ __forceinline__ uint32_t slow_code(const LutLds &T) {
+    template <int PEEK>
+    __device__ __forceinline__ uint32_t slow_code(const LutT<PEEK> &T) {
         const uint32_t hi = window();
         uint32_t u = __clz((int)hi), b, c;
         if (ELEM == kElemFp8 || u < kMaxRankBf16) {
@@ -343,7 +377,8 @@ struct Seq {
         step(s - c);
         return b;
     }
-    __device__ __forceinline__ void slow_quad(const LutLds &T, uint32_t &e1, uint32_t &e2) {
+    template <int PEEK>
+    __device__ __forceinline__ void slow_quad(const LutT<PEEK> &T, uint32_t &e1, uint32_t &e2) {
         uint32_t bytes = slow_code(T) << 24;                           // b3 b2 b1 b0 after four codes
 #pragma unroll 1
         for (int k = 1; k < 4; k++) bytes = (bytes >> 8) | (slow_code(T) << 24);
@@ -398,6 +433,7 @@ struct BlockArgs {
     uint32_t M, K;
     uint32_t G;             // row groups per workgroup
     uint32_t slot_words;    // LDS words per half-wave for a staged block (layouts 0/1)
+    const uint32_t *seq;    // 13-bit token-path decode table (nwc_seq_table) or null
 };
 
 struct GatherArgs {

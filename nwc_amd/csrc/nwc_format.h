@@ -16,6 +16,10 @@ constexpr uint32_t kBlock = kRows0 * kCols;   // nwc_info(4); the `block` argume
 constexpr uint32_t kHdrBytes = kLanes;        // one header byte per lane and block
 constexpr uint32_t kPeek = 12;                // LUT index bits
 constexpr uint32_t kLutWords = 1u << kPeek;
+// Token-path decode table with a 13-bit window (nwc_seq_table; not part of the format): 2^13 entries already in the
+// kernel's step encoding, then exp_of_rank[0..15] packed into four words.
+constexpr uint32_t kPeekSeq = 13;
+constexpr uint32_t kSeqTableWords = (1u << kPeekSeq) + 4u;
 constexpr uint32_t kMaxRankBf16 = 15;         // ranks 0..14 coded r zeros, 1, sign; 15 zeros + 1 = escape
 constexpr uint32_t kMaxRankFp8 = 10;          // fp8: 10 symbols, no escape
 constexpr uint32_t kFlag = 1u << 30;          // stored-LUT marker of an entry without two complete codes

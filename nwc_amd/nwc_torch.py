@@ -58,9 +58,13 @@ _lib.nwc_dequant.restype = I32; _lib.nwc_dequant.argtypes = [P, P, P, P, P, P, P
 _lib.nwc_linear_bf16.restype = I32
 _lib.nwc_linear_bf16.argtypes = [P, P, P, P, P, P, P, P, P, P, P, U64, U32, U32, I32]
 _lib.nwc_linear_xbf16.restype = I32
-_lib.nwc_linear_xbf16.argtypes = [P, P, P, P, P, P, P, P, P, P, P, U64, U32, I32]
+_lib.nwc_linear_xbf16.argtypes = [P, P, P, P, P, P, P, P, P, P, P, P, U64, U32, I32]
+_lib.nwc_seq_table.restype = I32
+_lib.nwc_seq_table.argtypes = [P, I32, P]
 _lib.nwc_row_index.restype = I32; _lib.nwc_row_index.argtypes = [P, P, P, P, P, P, P, U64, U32, I32]
 _lib.nwc_token_split.restype = I32; _lib.nwc_token_split.argtypes = [U64, U32, I32, I32]
+SEQ_TABLE = os.environ.get("NWC_SEQ_TABLE", "1") != "0"     # layout 0: the 13-bit token-path decode table
+SEQ_TABLE_WORDS = 8196
 ROW_INDEX = os.environ.get("NWC_ROW_INDEX", "1") != "0"   # layouts 0/1: build the row index for the token path
 _lib.nwc_gather.restype = I32; _lib.nwc_gather.argtypes = [P, P, P, P, P, P, P, U32, P, U64, U32, U32, I32]
 _lib.nwc_ref_fp8.restype = I32; _lib.nwc_ref_fp8.argtypes = [P, P, P, P, P, U64, U32]
@@ -102,8 +106,8 @@ def ref_fp8_matvec(w8: torch.Tensor, scale: torch.Tensor, x_f32: torch.Tensor) -
     _need_gpu(w8)
     M, K = w8.shape
     y = torch.empty(M, dtype=torch.bfloat16, device=w8.device)
-    xin = x_f32 if x_f32.numel() % 16 == 0 else F.pad(x_f32, (0, 16 - x_f32.numel() % 16))
-    err = _lib.nwc_ref_fp8(_stream(), _ptr(w8.view(torch.uint8)), _ptr(scale), _ptr(xin.contiguous()), _ptr(y), M, K)
+    xin = (x_f32 if x_f32.numel() % 16 == 0 else F.pad(x_f32, (0, 16 - x_f32.numel() % 16))).contiguous()
+    err = _lib.nwc_ref_fp8(_stream(), _ptr(w8.view(torch.uint8)), _ptr(scale), _ptr(xin), _ptr(y), M, K)
     if err:
         raise RuntimeError(f"nwc_ref_fp8 HIP error {err}")
     return y
@@ -284,11 +288,26 @@ class NWCWeight:
             self._row_index = ri
         return ri if ri is not False else None
 
+    def seq_table(self):
+        """Layout 0's 13-bit token-path decode table (int32 [8196] on the device, built on the host from the stored
+        LUT on first use; not part of the format), or None for layouts 1/2 or with NWC_SEQ_TABLE=0."""
+        if self.layout != 0 or not SEQ_TABLE:
+            return None
+        st = getattr(self, "_seq_table", None)
+        if st is None:
+            host = torch.empty(SEQ_TABLE_WORDS, dtype=torch.int32)
+            lut = self.lut.cpu().contiguous()                      # held: the library reads it through a raw pointer
+            if _lib.nwc_seq_table(_ptr(lut), self.code, _ptr(host)):
+                raise RuntimeError("nwc_seq_table failed")
+            st = self._seq_table = host.to(self.data.device)
+        return st
+
     def token_bytes(self):
         """Algorithmic bytes one token-path call reads: the compressed matrix, plus the row-index entries the kernel
-        uses: 64 bytes per block when it splits blocks over two half-waves (the middle entries), 192 over four."""
+        uses (64 bytes per block when it splits blocks over two half-waves, 192 over four) and the 13-bit table."""
         split = _lib.nwc_token_split(self.n, self.in_features, self.code, int(self.row_index() is not None))
-        return self.bytes + self.bases.numel() * LANES * 2 * (split - 1)
+        table = 4 * SEQ_TABLE_WORDS if self.seq_table() is not None else 0
+        return self.bytes + self.bases.numel() * LANES * 2 * (split - 1) + table
 
     def linear_bf16(self, x: torch.Tensor, bias) -> torch.Tensor:
         """Token path: y = scale * (W x) + bias, x BF16 or fp32, y BF16."""
@@ -298,9 +317,10 @@ class NWCWeight:
         sp = _ptr(self.scale) if self.scale is not None else None
         if x.dtype == torch.bfloat16 or self.layout:
             xin = self._x16(x if x.dtype == torch.bfloat16 else x.to(torch.bfloat16)).contiguous()
-            ri = self.row_index()
+            ri, st = self.row_index(), self.seq_table()
             err = _lib.nwc_linear_xbf16(_stream(), _ptr(self.data), _ptr(self.bases), _ptr(self.hdr), _ptr(self.lut),
-                                        _ptr(self.low), _ptr(ri) if ri is not None else None, _ptr(xin), bp, sp, _ptr(y),
+                                        _ptr(self.low), _ptr(ri) if ri is not None else None,
+                                        _ptr(st) if st is not None else None, _ptr(xin), bp, sp, _ptr(y),
                                         self.n, self.in_features, self.code)
         else:                                                      # layout 0 with fp32 activations: the reference ABI
             xin = self._x16(x.float()).contiguous()
