@@ -62,15 +62,15 @@ int nwc_linear_bf16(void *stream, const uint8_t *data, const uint32_t *bases, co
 
 /* Token path with x as BF16 for every layout (layout 0: BF16 [K16]; layouts 1/2: BF16 [K32]), otherwise as
  * nwc_linear_bf16.  row_index: the row index from nwc_row_index, or NULL; with it, small matrices decode each block
- * on two or four half-waves at once (same results).  seq_table: layout 0's 13-bit decode table from nwc_seq_table
- * (device, 8196 words), or NULL; with it fewer decode steps take the slow path (same results).  No counterpart in
+ * on two or four half-waves at once (same results).  seq_table: the 13-bit decode table of layouts 0/1 from
+ * nwc_seq_table (device, 8196 words), or NULL; with it fewer decode steps take the slow path (same results).  No counterpart in
  * the reference, whose Python side converts x to fp32 for layout 0 with an extra kernel (nwc_torch.py:238-239);
  * callers that hold BF16 activations use this one. */
 int nwc_linear_xbf16(void *stream, const uint8_t *data, const uint32_t *bases, const uint8_t *hdr, const uint32_t *tab,
                      const uint8_t *low, const uint16_t *row_index, const uint32_t *seq_table, const uint16_t *x,
                      const uint16_t *bias, const float *scale, uint16_t *y, uint64_t n, uint32_t K, int elem);
 
-/* Host: layout 0/1's 13-bit token-path decode table from a stored LUT (host copy of `tab`): out[0..8191] one entry
+/* Host: the 13-bit token-path decode table of layouts 0/1 from a stored LUT (host copy of `tab`): out[0..8191] one entry
  * per 13-bit window that starts with two complete codes ((17 - bits) | byte0 << 8 | byte1 << 16) or 0x40000000,
  * out[8192..8195] exp_of_rank[0..15].  Derived from the stored tensors once per matrix, not part of the format; 0,
  * or -1 for layout 2.  No counterpart in the reference. */

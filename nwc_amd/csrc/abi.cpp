@@ -125,7 +125,16 @@ bool plan_layout0_tiers(const Shape &f, int mode, int ncu, bool index, uint32_t 
 // caller then uses the multi-block kernel.
 constexpr uint32_t kSlotWords1s = 880, kSlotWords1Min = 768;
 constexpr uint32_t kDynLdsOne = 128u * 1024u;         // dynamic LDS of a workgroup that has its CU to itself
-bool plan_layout1(const Shape &f, int mode, int ncu, bool index, LaunchPlan &p) {
+constexpr uint32_t kDynLdsOne13 = 126u * 1024u;       // the same next to the 13-bit table
+bool plan_layout1_budget(const Shape &f, int mode, int ncu, bool index, uint32_t budget, uint32_t one, LaunchPlan &p);
+bool plan_layout1(const Shape &f, int mode, int ncu, bool index, bool seq, LaunchPlan &p) {
+    if (seq && mode == kToken && index && plan_layout1_budget(f, mode, ncu, index, kDynLds13, kDynLdsOne13, p)) {
+        p.seq13 = true;
+        return true;
+    }
+    return plan_layout1_budget(f, mode, ncu, index, kDynLdsPipe, kDynLdsOne, p);
+}
+bool plan_layout1_budget(const Shape &f, int mode, int ncu, bool index, uint32_t budget, uint32_t one, LaunchPlan &p) {
     p = LaunchPlan{};
     p.layout = 1;
     const bool rows = mode == kToken || mode == kF32;
@@ -136,8 +145,8 @@ bool plan_layout1(const Shape &f, int mode, int ncu, bool index, LaunchPlan &p) 
         const uint32_t halves = (blocks * sp + 1u) & ~1u;
         if (halves > 32u) continue;
         const uint32_t part = rows ? G * kRows12 * CB * sp * 4u + (f.K16 + 31u) / 32u * 64u : 0u;   // + x as BF16
-        if (part + blocks * kSlotWords1Min * 4u > kDynLdsPipe) continue;
-        const uint32_t slot = std::min(kSlotWords1s, (kDynLdsPipe - part) / (4u * blocks));
+        if (part + blocks * kSlotWords1Min * 4u > budget) continue;
+        const uint32_t slot = std::min(kSlotWords1s, (budget - part) / (4u * blocks));
         p.split = sp;
         p.G = G;
         p.threads = 32u * halves;
@@ -150,7 +159,7 @@ bool plan_layout1(const Shape &f, int mode, int ncu, bool index, LaunchPlan &p) 
     // workgroup per CU; the region copy moves at most 64 KB)
     if (index && mode == kToken && CB * 4u > 32u) {
         const uint32_t part = kRows12 * CB * 4u * 4u + (f.K16 + 31u) / 32u * 64u;
-        const uint32_t slot = std::min(kSlotWords1s, (kDynLdsOne - part) / (4u * CB));
+        const uint32_t slot = std::min(kSlotWords1s, (one - part) / (4u * CB));
         if (slot >= kSlotWords1Min && CB * kSlotWords1Min * 4u <= 64u * 1024u) {
             p.split = 4;
             p.multi = true;
@@ -170,7 +179,7 @@ bool plan_layout1(const Shape &f, int mode, int ncu, bool index, LaunchPlan &p) 
 // workgroup, and an even block count so both halves of every wave have a block.
 bool plan_blocks(const Shape &f, int layout, int mode, int ncu, bool index, LaunchPlan &p, bool seq = false) {
     if (layout == 0) return plan_layout0(f, mode, ncu, index, seq, p);
-    if (layout == 1 && plan_layout1(f, mode, ncu, index, p)) return true;
+    if (layout == 1 && plan_layout1(f, mode, ncu, index, seq, p)) return true;
     if (mode == kRowIndex) return false;
     p = LaunchPlan{};
     p.layout = layout;
@@ -205,7 +214,7 @@ int run_blocks(int mode, bool xbf16, hipStream_t st, const uint8_t *data, const 
     const int layout = elem_layout(elem), t = elem_type(elem);
     const Shape f((uint32_t)(n / K), K, layout);
     LaunchPlan p;
-    if (!plan_blocks(f, layout, mode, ncu, aux != nullptr && layout <= 1, p, seq != nullptr && layout == 0 && xbf16)) return -1;
+    if (!plan_blocks(f, layout, mode, ncu, aux != nullptr && layout <= 1, p, seq != nullptr && layout <= 1 && xbf16)) return -1;
     BlockArgs a{data, bases, hdr, tab, low, x, bias, scale, out, aux, f.M, f.K, p.G,
                 layout == 0 || p.split ? p.slot_words : slot_words_for(layout), seq};
     return layout == 2 ? launch_fixed(p, t, mode, xbf16, a, st) : launch_prefix(p, t, mode, xbf16, a, st);
@@ -241,7 +250,7 @@ extern "C" int nwc_linear_xbf16(void *stream, const uint8_t *data, const uint32_
                                 const uint16_t *bias, const float *scale, uint16_t *y, uint64_t n, uint32_t K, int elem) {
     if (!shape_ok(n, kBlock, K, elem)) return -1;
     return run_blocks(kToken, true, (hipStream_t)stream, data, bases, hdr, tab, low, x, bias, scale, y, n, K, elem,
-                      elem_layout(elem) <= 1 ? row_index : nullptr, elem_layout(elem) == 0 ? seq_table : nullptr);
+                      elem_layout(elem) <= 1 ? row_index : nullptr, elem_layout(elem) <= 1 ? seq_table : nullptr);
 }
 
 extern "C" int nwc_row_index(void *stream, const uint8_t *data, const uint32_t *bases, const uint8_t *hdr, const uint32_t *tab,

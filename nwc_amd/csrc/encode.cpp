@@ -448,7 +448,7 @@ extern "C" void nwc_build_tab(const uint16_t *freq, const uint16_t *psym, int el
     lut[1] = kFlag | (uint32_t)(psym[13] & 0x7F) << 8 | (uint32_t)(psym[14] & 0x7F) << 16;
 }
 
-// Token-path decode table of layout 0 with a 13-bit window, built from a stored LUT (its exp_of_rank): for every
+// Token-path decode table of layouts 0/1 with a 13-bit window, built from a stored LUT (its exp_of_rank): for every
 // 13-bit window that starts with two complete codes, (17 - c) | b0 << 8 | b1 << 16, the step encoding of the gfx950
 // kernel (byte 0 is the right shift that brings the second pair's 13 bits to [14:2]); for every other window the slow
 // marker 0x40000000.  out[8192..8195] hold exp_of_rank[0..15] (the slow path's rank -> byte map).  Not part of the

@@ -581,8 +581,8 @@ __device__ __forceinline__ void stage_x1(uint4 *xs, const void *x, uint32_t n8, 
 // Raw super-chunks in flight per half-wave in the single-round kernel: two, as for layout 0's rows.
 constexpr int kRing1 = 2;
 // NEXT (NS = 4, several items per half-wave): each ring slot is refilled with the next item's super-chunk once used.
-template <int ELEM, int MODE, int NS, bool FULL, bool NEXT = false>
-__device__ __forceinline__ float2 chunks1(const LutLds &s, const uint32_t *lane, uint32_t P0, const BlockArgs &a,
+template <int ELEM, int MODE, int NS, bool FULL, bool NEXT = false, class Tab>
+__device__ __forceinline__ float2 chunks1(const Tab &s, const uint32_t *lane, uint32_t P0, const BlockArgs &a,
                                           const Shape &f, const uint4 *xs, uint4 ring[4], const Coord1 &c, uint32_t sc0,
                                           uint32_t L, const Coord1 *cn = nullptr, uint32_t nsc0 = 0) {
     static_assert(!NEXT || NS == 4, "next-item refills for four-super-chunk items");
@@ -648,8 +648,8 @@ __device__ __forceinline__ float2 chunks1(const LutLds &s, const uint32_t *lane,
 
 // chunks1 for a block whose tile does not fit the region buffer (and for building the row index): from global memory,
 // with a rolled loop and one raw load per super-chunk (compact code for a rare path).
-template <int ELEM, int MODE, int NS>
-__device__ __forceinline__ float2 chunks1_global(const LutLds &s, const uint32_t *lane, uint32_t P0, const BlockArgs &a,
+template <int ELEM, int MODE, int NS, class Tab>
+__device__ __forceinline__ float2 chunks1_global(const Tab &s, const uint32_t *lane, uint32_t P0, const BlockArgs &a,
                                                  const uint4 *xs, const Coord1 &c, uint32_t sc0, uint32_t L) {
     Seq<ELEM> S;
     S.init_at(lane, P0);
@@ -690,11 +690,11 @@ __device__ __forceinline__ float2 chunks1_global(const LutLds &s, const uint32_t
     return make_float2(accA, accB);
 }
 
-template <int ELEM, int MODE, bool XBF16, int NS, bool FULL>
+template <int ELEM, int MODE, bool XBF16, int NS, bool FULL, int PEEK = kPeek>
 __global__ void __launch_bounds__(1024) k_layout1s(BlockArgs a) {
     constexpr uint32_t SP = 16u / NS;                          // half-waves per block
     constexpr bool ROWS = MODE == kToken || MODE == kF32;
-    __shared__ LutLds s;
+    __shared__ LutT<PEEK> s;
     extern __shared__ uint32_t dyn[];
     const uint32_t tid = threadIdx.x, nth = blockDim.x, L = tid & 31;
     const uint32_t hw = tid >> 5, H = nth >> 5, HB = H / SP;
@@ -710,8 +710,8 @@ __global__ void __launch_bounds__(1024) k_layout1s(BlockArgs a) {
     const uint32_t B0 = rg0 * f.CB, nb = f.nb;
     const uint32_t mend = B0 + nt == nb ? matrix_end(a, nb) : 0u;
     Region R = region_of(a, B0, B0 + nt, nb, mend);
-    LutLoad Q;
-    lut_issue(Q, a.lut);
+    TabStage<PEEK> Q;
+    Q.issue(a);
     const uint32_t t = hw / SP, p = hw % SP, sc0 = p * NS;
     const Coord1 c = coord1<ELEM>(min(t, tl), rg0, f, L);
     const uint32_t n = a.hdr[(uint64_t)c.b * kHdrBytes + L], base = a.bases[c.b];
@@ -719,7 +719,7 @@ __global__ void __launch_bounds__(1024) k_layout1s(BlockArgs a) {
     Bulk Bk;
     bulk_issue(Bk, a.data, R, tid, nth);
     if (ROWS) stage_x1<XBF16>(xs, a.x, n8, tid, nth);
-    lut_commit<kLutSeq>(s, Q, a.lut);
+    Q.commit(s, a);
     uint4 ring[4];
 #pragma unroll
     for (int i = 0; i < kRing1; i++) ring[i] = MODE == kRowIndex ? make_uint4(0u, 0u, 0u, 0u) : raw1<ELEM>(a.low, c, sc0 + i);
@@ -749,11 +749,11 @@ __global__ void __launch_bounds__(1024) k_layout1s(BlockArgs a) {
 // group (its streams staged once, up to ~90 KB of LDS), and its items (block, quarter of the super-chunks) go
 // round-robin to 32 half-waves; while an item decodes, the next item's raw super-chunks, header byte, base and
 // row-index entry are requested, so a half-wave never waits for global memory between items.
-template <int ELEM, bool FULL>
+template <int ELEM, bool FULL, int PEEK = kPeek>
 __global__ void __launch_bounds__(1024) k_layout1m(BlockArgs a) {
     constexpr int MODE = kToken;
     constexpr uint32_t NS = 4, SP = 4;
-    __shared__ LutLds s;
+    __shared__ LutT<PEEK> s;
     extern __shared__ uint32_t dyn[];
     const uint32_t tid = threadIdx.x, nth = blockDim.x, L = tid & 31;
     const uint32_t hw = tid >> 5, H = nth >> 5;
@@ -769,8 +769,8 @@ __global__ void __launch_bounds__(1024) k_layout1m(BlockArgs a) {
     const uint32_t B0 = rg0 * f.CB, nb = f.nb;
     const uint32_t mend = B0 + nt == nb ? matrix_end(a, nb) : 0u;
     Region R = region_of(a, B0, B0 + nt, nb, mend);
-    LutLoad Q;
-    lut_issue(Q, a.lut);
+    TabStage<PEEK> Q;
+    Q.issue(a);
     const uint32_t ntot = nt * SP, itl = ntot - 1u;
     auto item = [&](uint32_t it, Coord1 &c, uint32_t &p) {
         const uint32_t i = min(it, itl);
@@ -785,7 +785,7 @@ __global__ void __launch_bounds__(1024) k_layout1m(BlockArgs a) {
     Bulk Bk;
     bulk_issue(Bk, a.data, R, tid, nth);
     stage_x1<true>(xs, a.x, n8, tid, nth);
-    lut_commit<kLutSeq>(s, Q, a.lut);
+    Q.commit(s, a);
     uint4 ring[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) ring[i] = raw1<ELEM>(a.low, c, p * NS + i);
@@ -939,33 +939,44 @@ __global__ void __launch_bounds__(256) k_gather1(GatherArgs a) {
 }
 
 // ---------------------------------------------------------------------------------------------------------------
-// Layout 1, single round: FULL when every block codes all 16 super-chunks (K a multiple of 512).
+// Layout 1 token path (BF16 x, row index): the multi-item kernel or the single-round kernel with a 4 or 8
+// super-chunk split, with the stored 12-bit LUT or the 13-bit table.  FULL when every block codes all 16
+// super-chunks (K a multiple of 512).
+template <int ELEM, int PEEK>
+static int launch_layout1_token(const LaunchPlan &p, const BlockArgs &a, hipStream_t st, bool full) {
+    const dim3 g(p.grid), b(p.threads);
+    if (p.multi) {
+        // more than 64 KB of LDS: raise the kernel's limit (idempotent, so concurrent first calls are fine)
+        auto kf = full ? (const void *)k_layout1m<ELEM, true, PEEK> : (const void *)k_layout1m<ELEM, false, PEEK>;
+        if (p.lds > 64u * 1024u) {
+            const hipError_t e = hipFuncSetAttribute(kf, hipFuncAttributeMaxDynamicSharedMemorySize, (int)p.lds);
+            if (e != hipSuccess) return (int)e;
+        }
+        if (full) hipLaunchKernelGGL((k_layout1m<ELEM, true, PEEK>), g, b, p.lds, st, a);
+        else hipLaunchKernelGGL((k_layout1m<ELEM, false, PEEK>), g, b, p.lds, st, a);
+        return (int)hipGetLastError();
+    }
+    if (p.split == 4) {
+        if (full) hipLaunchKernelGGL((k_layout1s<ELEM, kToken, true, 4, true, PEEK>), g, b, p.lds, st, a);
+        else hipLaunchKernelGGL((k_layout1s<ELEM, kToken, true, 4, false, PEEK>), g, b, p.lds, st, a);
+        return (int)hipGetLastError();
+    }
+    if (p.split == 2) {
+        if (full) hipLaunchKernelGGL((k_layout1s<ELEM, kToken, true, 8, true, PEEK>), g, b, p.lds, st, a);
+        else hipLaunchKernelGGL((k_layout1s<ELEM, kToken, true, 8, false, PEEK>), g, b, p.lds, st, a);
+        return (int)hipGetLastError();
+    }
+    return -1;
+}
+
+// Layout 1, single round.
 template <int ELEM, int MODE, bool XBF16>
 static int launch_layout1s(const LaunchPlan &p, const BlockArgs &a, hipStream_t st) {
     const bool full = Shape(a.M, a.K, 1).nsl == 16u;
     const dim3 g(p.grid), b(p.threads);
-    if constexpr (MODE == kToken && XBF16) {                   // the entry point that takes the row index
-        if (p.multi) {
-            // more than 64 KB of dynamic LDS: raise the kernel's limit (idempotent, so concurrent first calls are fine)
-            auto kf = full ? (const void *)k_layout1m<ELEM, true> : (const void *)k_layout1m<ELEM, false>;
-            if (p.lds > 64u * 1024u) {
-                const hipError_t e = hipFuncSetAttribute(kf, hipFuncAttributeMaxDynamicSharedMemorySize, (int)p.lds);
-                if (e != hipSuccess) return (int)e;
-            }
-            if (full) hipLaunchKernelGGL((k_layout1m<ELEM, true>), g, b, p.lds, st, a);
-            else hipLaunchKernelGGL((k_layout1m<ELEM, false>), g, b, p.lds, st, a);
-            return (int)hipGetLastError();
-        }
-        if (p.split == 4) {
-            if (full) hipLaunchKernelGGL((k_layout1s<ELEM, MODE, XBF16, 4, true>), g, b, p.lds, st, a);
-            else hipLaunchKernelGGL((k_layout1s<ELEM, MODE, XBF16, 4, false>), g, b, p.lds, st, a);
-            return (int)hipGetLastError();
-        }
-        if (p.split == 2) {
-            if (full) hipLaunchKernelGGL((k_layout1s<ELEM, MODE, XBF16, 8, true>), g, b, p.lds, st, a);
-            else hipLaunchKernelGGL((k_layout1s<ELEM, MODE, XBF16, 8, false>), g, b, p.lds, st, a);
-            return (int)hipGetLastError();
-        }
+    if constexpr (MODE == kToken && XBF16) {                   // the entry point that takes the row index and table
+        if (p.seq13) return launch_layout1_token<ELEM, kPeekSeq>(p, a, st, full);
+        return launch_layout1_token<ELEM, kPeek>(p, a, st, full);
     }
     if constexpr (MODE == kRowIndex) {
         if (p.split != 1) return -1;

@@ -289,9 +289,9 @@ class NWCWeight:
         return ri if ri is not False else None
 
     def seq_table(self):
-        """Layout 0's 13-bit token-path decode table (int32 [8196] on the device, built on the host from the stored
-        LUT on first use; not part of the format), or None for layouts 1/2 or with NWC_SEQ_TABLE=0."""
-        if self.layout != 0 or not SEQ_TABLE:
+        """The 13-bit token-path decode table of layouts 0/1 (int32 [8196] on the device, built on the host from the
+        stored LUT on first use; not part of the format), or None for layout 2 or with NWC_SEQ_TABLE=0."""
+        if self.layout > 1 or not SEQ_TABLE:
             return None
         st = getattr(self, "_seq_table", None)
         if st is None:

@@ -267,13 +267,11 @@ def test_token_path_with_and_without_row_index(cuda, layout, M, K, split, escape
     x = torch.randn(K, generator=torch.Generator().manual_seed(6)).to(torch.bfloat16).cuda()
     xin = c._x16(x).contiguous()                             # zero-padded to K16 (layout 0) or K32 (layout 1)
     ys = []
-    combos = [(c.row_index(), None), (None, None)]
-    if layout == 0:                                          # and with the 13-bit decode table
-        host = torch.zeros(c.seq_table().numel(), dtype=torch.int32)
-        lut = c.lut.cpu()
-        assert _lib.nwc_seq_table(_ptr(lut), c.code, _ptr(host)) == 0
-        assert torch.equal(c.seq_table().cpu(), host)        # the device copy is the host build
-        combos += [(c.row_index(), c.seq_table()), (None, c.seq_table())]
+    host = torch.zeros(c.seq_table().numel(), dtype=torch.int32)
+    lut = c.lut.cpu()
+    assert _lib.nwc_seq_table(_ptr(lut), c.code, _ptr(host)) == 0
+    assert torch.equal(c.seq_table().cpu(), host)            # the device copy of the 13-bit table is the host build
+    combos = [(c.row_index(), None), (None, None), (c.row_index(), c.seq_table()), (None, c.seq_table())]
     for ri, st in combos:
         y = torch.empty(M, dtype=torch.bfloat16, device="cuda")
         err = _lib.nwc_linear_xbf16(_stream(), _ptr(c.data), _ptr(c.bases), _ptr(c.hdr), _ptr(c.lut), _ptr(c.low),
@@ -281,8 +279,7 @@ def test_token_path_with_and_without_row_index(cuda, layout, M, K, split, escape
                                     _ptr(xin), None, None, _ptr(y), c.n, K, c.code)
         assert err == 0
         ys.append(y.double().cpu().numpy())
-    if layout == 0:                                          # the table changes no sum: bit-identical
-        assert np.array_equal(ys[2], ys[0]) and np.array_equal(ys[3], ys[1])
+    assert np.array_equal(ys[2], ys[0]) and np.array_equal(ys[3], ys[1])   # the table changes no sum: bit-identical
     y64 = (w.cuda().double() @ x.double()).cpu().numpy()
     for y in ys:
         assert np.all(np.abs(y - y64) <= 2.0 ** -8 * np.abs(y64) + 1e-5)

@@ -126,7 +126,7 @@ def test_weight_seq_table_is_the_host_build():
     NWCWeight, _, _, _ = _nwc()
     c = NWCWeight(bf16_matrix(16, 1024, seed=2), device="cpu", layout=0)
     assert np.array_equal(c.seq_table().numpy().view(np.uint32), _table(c))
-    assert NWCWeight(bf16_matrix(16, 1024, seed=2), device="cpu", layout=1).seq_table() is None
+    assert NWCWeight(bf16_matrix(16, 1024, seed=2), device="cpu", layout=2).seq_table() is None
 
 
 def test_seq_table_rejects_layout2():
