@@ -177,13 +177,30 @@ bool plan_layout1_budget(const Shape &f, int mode, int ncu, bool index, uint32_t
 // Layouts 1/2: workgroup tile = G whole row groups, one block per half-wave where the LDS budget allows.  Prefer at
 // least two workgroups per CU (small matrices spread over the whole chip), at most 32 blocks (16 waves) per
 // workgroup, and an even block count so both halves of every wave have a block.
-bool plan_blocks(const Shape &f, int layout, int mode, int ncu, bool index, LaunchPlan &p, bool seq = false) {
+bool plan_blocks(const Shape &f, int layout, int mode, int ncu, bool index, LaunchPlan &p, bool seq = false,
+                 bool fp8 = false) {
     if (layout == 0) return plan_layout0(f, mode, ncu, index, seq, p);
     if (layout == 1 && plan_layout1(f, mode, ncu, index, seq, p)) return true;
     if (mode == kRowIndex) return false;
     p = LaunchPlan{};
     p.layout = layout;
     const uint32_t CB = f.CB, groups = f.groups(), slot = slot_words_for(layout);
+    // layout 2, BF16 token path, few row groups per CU: four or two half-waves per block (super-chunk ranges), one
+    // round (the token path of layouts 1/2 always takes BF16 x)
+    if (layout == 2 && !fp8 && mode == kToken) {
+        const uint32_t G = std::max(1u, (groups + 2u * (uint32_t)ncu - 1u) / (2u * (uint32_t)ncu));
+        for (uint32_t sp : {4u, 2u}) {
+            const uint32_t halves = (G * CB * sp + 1u) & ~1u;
+            const uint32_t lds = (f.K16 + 31u) / 32u * 64u + G * f.rows * CB * sp * 4u;   // x as BF16, partial sums
+            if (halves > 32u || lds > kDynLdsPipe) continue;
+            p.split = sp;
+            p.G = G;
+            p.threads = 32u * halves;
+            p.grid = (groups + G - 1u) / G;
+            p.lds = lds;
+            return true;
+        }
+    }
     uint32_t G = CB >= 32 ? 1u : 32u / CB;
     while (G > 1 && (groups + G - 1) / G < 2u * (uint32_t)ncu) G--;
     if (G > 1 && ((G * CB) & 1u)) G--;
@@ -214,7 +231,9 @@ int run_blocks(int mode, bool xbf16, hipStream_t st, const uint8_t *data, const 
     const int layout = elem_layout(elem), t = elem_type(elem);
     const Shape f((uint32_t)(n / K), K, layout);
     LaunchPlan p;
-    if (!plan_blocks(f, layout, mode, ncu, aux != nullptr && layout <= 1, p, seq != nullptr && layout <= 1 && xbf16)) return -1;
+    if (!plan_blocks(f, layout, mode, ncu, aux != nullptr && layout <= 1, p, seq != nullptr && layout <= 1 && xbf16,
+                     t == kElemFp8))
+        return -1;
     BlockArgs a{data, bases, hdr, tab, low, x, bias, scale, out, aux, f.M, f.K, p.G,
                 layout == 0 || p.split ? p.slot_words : slot_words_for(layout), seq};
     return layout == 2 ? launch_fixed(p, t, mode, xbf16, a, st) : launch_prefix(p, t, mode, xbf16, a, st);

@@ -201,6 +201,88 @@ __global__ void __launch_bounds__(1024) k_layout2(BlockArgs a) {
     if (MODE != kDequant) finish_rows<MODE>(a, part, rg0 * kRows12, ng * kRows12, f.CB);
 }
 
+// BF16 token / fp32 paths, single round: a workgroup owns G whole 16-row groups; each half-wave decodes super-chunks
+// sc0 .. sc0 + NS - 1 of one block (SP = 16 / NS half-waves per block, so small matrices still fill the CUs), with its
+// nibble and raw loads four super-chunks ahead, the BF16 activations staged once per workgroup in LDS, and its lane's
+// exceptions whose super-chunk lies in its range (the fp32 path keeps k_layout2 and its fp32 products).  Partial row sums per (row, column block, part), summed in a fixed
+// order by the workgroup.  The fixed-width format needs no index to start inside a block.
+template <int MODE, bool XBF16, int NS>
+__global__ void __launch_bounds__(1024) k_layout2s(BlockArgs a) {
+    static_assert(NS == 4 || NS == 8, "four or two half-waves per block");
+    static_assert(MODE == kToken && XBF16, "the BF16 token path");
+    constexpr uint32_t SP = 16u / NS, R = 4;
+    extern __shared__ uint32_t dyn[];
+    const RankTab tab{a.lut[0], a.lut[1], a.lut[2], a.lut[3]};
+    constexpr uint32_t esz = 3u;
+    const uint32_t tid = threadIdx.x, nth = blockDim.x, L = tid & 31, r = L >> 2, q = L & 3;
+    const uint32_t hw = tid >> 5, H = nth >> 5;
+    const Shape f(a.M, a.K, 2);
+    const uint32_t n8 = (f.K16 + 31u) / 32u * 4u;                   // x: K32 BF16 values, in chunks of eight
+    uint4 *xs = (uint4 *)dyn;
+    float *part = (float *)(xs + n8);
+    const uint8_t *rplane = a.low + f.nib2_bytes();
+    const uint32_t rg0 = blockIdx.x * a.G;
+    const uint32_t ng = min(a.G, f.groups() - rg0);
+    const uint32_t nt = ng * f.CB;
+    for (uint32_t i = tid; i < n8; i += nth) xs[i] = ((const uint4 *)a.x)[i];
+    __syncthreads();
+    for (uint32_t it = hw; it < nt * SP; it += H) {
+        const uint32_t t = it / SP, p = it - t * SP;
+        const uint32_t g = t / f.CB, cb = t - g * f.CB, rb = rg0 + g, b = rb * f.CB + cb;
+        const uint32_t nsc = ((cb == f.CB - 1 ? f.nl : 32u) + 1) / 2, slot0 = rb * f.spr + cb * 16;
+        const uint32_t sc0 = p * NS, ns = sc0 < nsc ? min(NS, nsc - sc0) : 0u;
+        const uint8_t *np = a.low + ((uint64_t)(slot0 + sc0) * kLanes + L) * 8;
+        const uint8_t *rp = rplane + ((uint64_t)(slot0 + sc0) * kLanes + L) * 16;
+        // the ring: super-chunk i of the range in slot i % R; loads past the range re-read its last super-chunk
+        uint2 nr[R];
+        uint4 rr[R];
+        const uint32_t last = ns ? ns - 1u : 0u;
+#pragma unroll
+        for (uint32_t i = 0; i < R; i++) {
+            nr[i] = ldnt2(np + (uint64_t)min(i, last) * kLanes * 8);
+            rr[i] = ldnt4(rp + (uint64_t)min(i, last) * kLanes * 16);
+        }
+        float accA = 0.f, accB = 0.f;
+#pragma unroll
+        for (uint32_t i = 0; i < NS; i++) {
+            if (i >= ns) continue;                               // a last column block's missing super-chunks
+            uint32_t pa[4], qa[4];
+            decode_sc<kElemBf16, 0>(tab, nullptr, nr[i % R], rr[i % R], 0u, 0u, 0u, pa, qa);
+            if (i + R < NS) {
+                nr[i % R] = ldnt2(np + (uint64_t)min(i + R, last) * kLanes * 8);
+                rr[i % R] = ldnt4(rp + (uint64_t)min(i + R, last) * kLanes * 16);
+            }
+            const uint4 xv = xs[(cb * kCols + (sc0 + i) * 32u + 8u * q) >> 3];
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                accA = dot2_bf16(pa[k], u4_get(xv, k), accA);
+                accB = dot2_bf16(qa[k], u4_get(xv, k), accB);
+            }
+            asm volatile("" : "+v"(accA), "+v"(accB));
+        }
+        // exceptions of this lane whose super-chunk is in the range (planes decoded to +-0, the entries carry the value)
+        uint32_t cnt;
+        const uint8_t *ep = exc_start(a, b, L, esz, cnt);
+        for (uint32_t k = 0; k < cnt; k++, ep += esz) {
+            const uint32_t i = ep[0], j = i & 15, sc = i >> 4;
+            if (sc - sc0 >= ns) continue;
+            const uint32_t col = cb * kCols + sc * 32 + frag_col(L, j), upper = (j >> 1) & 1u;
+            const float w = exc_value<kElemBf16>(ep);
+            const float xv = __uint_as_float((uint32_t)((const uint16_t *)xs)[col] << 16);
+            if (upper) accB = fmaf(w, xv, accB);
+            else accA = fmaf(w, xv, accA);
+        }
+        accA += xor_f<1>(accA); accA += xor_f<2>(accA);
+        accB += xor_f<1>(accB); accB += xor_f<2>(accB);
+        if (q == 0) {
+            const uint32_t pi = ((g * kRows12 + r) * f.CB + cb) * SP + p;
+            part[pi] = accA;
+            part[pi + 8u * f.CB * SP] = accB;
+        }
+    }
+    finish_rows<MODE>(a, part, rg0 * kRows12, ng * kRows12, f.CB * SP);
+}
+
 // Row gather: one half-wave per requested row; the row's lanes store their columns, then patch their exceptions.
 template <int ELEM>
 __global__ void __launch_bounds__(256) k_gather2(GatherArgs a) {
@@ -257,6 +339,13 @@ __global__ void __launch_bounds__(256) k_gather2(GatherArgs a) {
 
 template <int ELEM, int MODE, bool XBF16>
 static int launch_fixed_t(const LaunchPlan &p, const BlockArgs &a, hipStream_t st) {
+    if constexpr (ELEM == kElemBf16 && MODE == kToken && XBF16) {
+        if (p.split) {
+            if (p.split == 4) hipLaunchKernelGGL((k_layout2s<MODE, XBF16, 4>), dim3(p.grid), dim3(p.threads), p.lds, st, a);
+            else hipLaunchKernelGGL((k_layout2s<MODE, XBF16, 8>), dim3(p.grid), dim3(p.threads), p.lds, st, a);
+            return (int)hipGetLastError();
+        }
+    }
     hipLaunchKernelGGL((k_layout2<ELEM, MODE, XBF16>), dim3(p.grid), dim3(p.threads), p.lds, st, a);
     return (int)hipGetLastError();
 }

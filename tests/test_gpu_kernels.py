@@ -283,3 +283,26 @@ def test_token_path_with_and_without_row_index(cuda, layout, M, K, split, escape
     y64 = (w.cuda().double() @ x.double()).cpu().numpy()
     for y in ys:
         assert np.all(np.abs(y - y64) <= 2.0 ** -8 * np.abs(y64) + 1e-5)
+
+
+@pytest.mark.parametrize("M,K,escapes", [(4608, 3584, "none"), (3584, 3584, "dense"), (1003, 1100, "dense"),
+                                          (16, 512, "none"), (2000, 3000, "dense")])
+def test_layout2_split_token_path(cuda, M, K, escapes):
+    """Layout 2's token path on matrices with few 16-row groups per CU, where a block's 16 super-chunks go to four or
+    two half-waves (qkv / o of Qwen2.5-7B, ragged shapes), against float64 on the decoded weights and against the
+    fp32 path's whole-block kernel; "dense" places runs of exceptions (ranks past the table) in several super-chunks of
+    one lane, so each part must add exactly the exceptions of its own range."""
+    NWCWeight, _, _ = _nwc()
+    w = bf16_matrix(M, K, seed=11, escapes=False)
+    if escapes == "dense":
+        big = torch.tensor(1e30, dtype=torch.bfloat16)
+        w[0, 0:512:3] = big                                   # one lane-row, many super-chunks
+        w[9, 600:700] = -big
+        w[M - 1, K - 40:K] = big
+    c = NWCWeight(w, device="cuda", layout=2)
+    x = torch.randn(K, generator=torch.Generator().manual_seed(12)).to(torch.bfloat16)
+    y = c.linear_bf16(x.cuda(), None).double().cpu().numpy()
+    y64 = (w.double() @ x.double()).numpy()
+    assert np.all(np.abs(y - y64) <= 2.0 ** -8 * np.abs(y64) + 1e-5)
+    y32 = c.matvec(x.float().cuda()).double().cpu().numpy()       # fp32 path: the whole-block kernel
+    assert np.all(np.abs(y - y32) <= 2.0 ** -8 * np.abs(y32) + 1e-5)
