@@ -220,6 +220,14 @@ bool plan_blocks(const Shape &f, int layout, int mode, int ncu, bool index, Laun
     p.threads = 32u * halves;
     p.grid = (groups + G - 1) / G;
     p.lds = lds_of(G, halves);
+    if (layout == 2 && !fp8 && mode == kToken) {        // the single-round kernel with one half-wave per block
+        // (activations staged in LDS and loads four super-chunks ahead: 7B gate_up 47.6 -> 43.6 us, down 27.6 -> 25.9)
+        const uint32_t xb = (f.K16 + 31u) / 32u * 64u;
+        if (p.lds + xb <= kDynLdsPipe) {
+            p.split = 1;
+            p.lds += xb;
+        }
+    }
     return true;
 }
 

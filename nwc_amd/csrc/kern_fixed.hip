@@ -201,14 +201,15 @@ __global__ void __launch_bounds__(1024) k_layout2(BlockArgs a) {
     if (MODE != kDequant) finish_rows<MODE>(a, part, rg0 * kRows12, ng * kRows12, f.CB);
 }
 
-// BF16 token / fp32 paths, single round: a workgroup owns G whole 16-row groups; each half-wave decodes super-chunks
-// sc0 .. sc0 + NS - 1 of one block (SP = 16 / NS half-waves per block, so small matrices still fill the CUs), with its
+// BF16 token path: a workgroup owns G whole 16-row groups; each half-wave decodes super-chunks sc0 .. sc0 + NS - 1
+// of a block (SP = 16 / NS half-waves per block, so small matrices still fill the CUs; several blocks in turn when
+// the tile has more than fit), with its
 // nibble and raw loads four super-chunks ahead, the BF16 activations staged once per workgroup in LDS, and its lane's
 // exceptions whose super-chunk lies in its range (the fp32 path keeps k_layout2 and its fp32 products).  Partial row sums per (row, column block, part), summed in a fixed
 // order by the workgroup.  The fixed-width format needs no index to start inside a block.
 template <int MODE, bool XBF16, int NS>
 __global__ void __launch_bounds__(1024) k_layout2s(BlockArgs a) {
-    static_assert(NS == 4 || NS == 8, "four or two half-waves per block");
+    static_assert(NS == 4 || NS == 8 || NS == 16, "four, two or one half-wave per block");
     static_assert(MODE == kToken && XBF16, "the BF16 token path");
     constexpr uint32_t SP = 16u / NS, R = 4;
     extern __shared__ uint32_t dyn[];
@@ -342,7 +343,8 @@ static int launch_fixed_t(const LaunchPlan &p, const BlockArgs &a, hipStream_t s
     if constexpr (ELEM == kElemBf16 && MODE == kToken && XBF16) {
         if (p.split) {
             if (p.split == 4) hipLaunchKernelGGL((k_layout2s<MODE, XBF16, 4>), dim3(p.grid), dim3(p.threads), p.lds, st, a);
-            else hipLaunchKernelGGL((k_layout2s<MODE, XBF16, 8>), dim3(p.grid), dim3(p.threads), p.lds, st, a);
+            else if (p.split == 2) hipLaunchKernelGGL((k_layout2s<MODE, XBF16, 8>), dim3(p.grid), dim3(p.threads), p.lds, st, a);
+            else hipLaunchKernelGGL((k_layout2s<MODE, XBF16, 16>), dim3(p.grid), dim3(p.threads), p.lds, st, a);
             return (int)hipGetLastError();
         }
     }
