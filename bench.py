@@ -23,7 +23,8 @@ The other BASELINE configs, each printed as one JSON line of its own (not the dr
                            tokens, against the GEMM on resident BF16 weights
   --gather 64              configs[4] embedding: 64 seeded ids from the 152064x3584 table, layouts 0, 1 and 2
 usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--layout 0] [--cpu-seconds 10] [--config NAME]
-       python bench.py --profile-launches 20     (counter target for rocprofv3 --pmc: copies + gate_up launches)
+       python bench.py --profile-launches 20     (counter target for rocprofv3 --pmc: copies + gate_up launches;
+                                                 --profile-shape qkv|o|gate_up|down picks the matrix)
 """
 import argparse
 import ctypes
@@ -391,8 +392,9 @@ def traffic_bytes():
 
 
 def run_profile(args):
-    """Counter target: --profile-launches gate_up launches, after three device copies of 256 MiB (the calibration
-    kernel of known size).  Run under rocprofv3 --pmc; prints one line per phase."""
+    """Counter target: --profile-launches launches of one Qwen3-4B matrix (--profile-shape, default gate_up), after
+    three device copies of 256 MiB (the calibration kernel of known size).  Run under rocprofv3 --pmc; prints one line
+    per phase."""
     import torch
     from nwc_amd.nwc_torch import NWCWeight
     dev = torch.device("cuda:0")
@@ -403,8 +405,8 @@ def run_profile(args):
     torch.cuda.synchronize()
     print("calibration: 3 copies of 268435456 bytes", flush=True)
     del src, dst
-    name, M, K = next(s for s in SHAPES if s[0] == DOMINANT)
-    c = NWCWeight(make_weight(M, K, 1000 + [s[0] for s in SHAPES].index(DOMINANT)), device=dev, layout=args.layout)
+    name, M, K = next(s for s in SHAPES if s[0] == args.profile_shape)
+    c = NWCWeight(make_weight(M, K, 1000 + [s[0] for s in SHAPES].index(name)), device=dev, layout=args.layout)
     cs = [c] + [clone_weight(c) for _ in range(7)]
     x = torch.randn(K, generator=torch.Generator().manual_seed(2)).to(torch.bfloat16).to(dev)
     ys = [torch.empty(M, dtype=torch.bfloat16, device=dev) for _ in cs]
@@ -413,7 +415,7 @@ def run_profile(args):
     for i in range(args.profile_launches):
         L[i % len(L)](sh)
     torch.cuda.synchronize()
-    print(f"{DOMINANT}: {args.profile_launches} launches, {c.token_bytes() + 2 * K + 2 * M} algorithmic bytes each", flush=True)
+    print(f"{name}: {args.profile_launches} launches, {c.token_bytes() + 2 * K + 2 * M} algorithmic bytes each", flush=True)
 
 
 def main():
@@ -428,6 +430,8 @@ def main():
     ap.add_argument("--no-baseline", action="store_true")
     ap.add_argument("--profile-launches", type=int, default=0,
                     help="only run the counter target (copies + this many gate_up launches), for rocprofv3 --pmc")
+    ap.add_argument("--profile-shape", default=DOMINANT, choices=[s[0] for s in SHAPES],
+                    help="the Qwen3-4B matrix --profile-launches runs")
     ap.add_argument("--config", default="qwen3-4b", choices=sorted(CONFIGS))
     ap.add_argument("--prefill", type=int, default=0, help="time the prefill path for this many tokens instead")
     ap.add_argument("--gather", type=int, default=0, help="time the embedding gather of this many ids instead")
