@@ -292,16 +292,17 @@ __global__ void __launch_bounds__(256) k_gather2(GatherArgs a) {
     const RankTab tab{a.lut[0], a.lut[1], a.lut[2], a.lut[3]};
     constexpr uint32_t esz = ELEM == kElemFp8 ? 2u : 3u;
     const uint32_t L = threadIdx.x & 31, r = L >> 2, q = L & 3;
-    const uint32_t id = blockIdx.x * (blockDim.x >> 5) + (threadIdx.x >> 5);
+    const Shape f(a.M, a.K, 2);
+    // one half-wave per (id, column block): the blocks of a row decode in parallel
+    const uint32_t item = blockIdx.x * (blockDim.x >> 5) + (threadIdx.x >> 5), id = item / f.CB, cb = item - id * f.CB;
     if (id >= a.n_ids) return;
     const int64_t R = a.ids[id];
     if (R < 0 || R >= (int64_t)a.M) return;
-    const Shape f(a.M, a.K, 2);
     const uint8_t *rplane = a.low + f.nib2_bytes();
     const uint32_t rb = (uint32_t)R / kRows12, rr = (uint32_t)R % kRows12;
     const bool mine = (rr & 7u) == r, upper = rr >= 8;
     uint16_t *o = a.out + (uint64_t)id * f.K16;
-    for (uint32_t cb = 0; cb < f.CB; cb++) {
+    {
         const uint32_t nsc = ((cb == f.CB - 1 ? f.nl : 32u) + 1) / 2, slot0 = rb * f.spr + cb * 16;
         const uint8_t *np = a.low + ((uint64_t)slot0 * kLanes + L) * 8;
         const uint8_t *rp = ELEM == kElemFp8 ? rplane + (((uint64_t)rb * f.spr2 + cb * 8) * 3 * kLanes + L) * 4
@@ -364,8 +365,9 @@ int launch_fixed(const LaunchPlan &p, int elem_t, int mode, bool xbf16, const Bl
 }
 
 int launch_gather_fixed(int elem_t, const GatherArgs &a, hipStream_t st) {
-    const uint32_t per = 8;
-    const dim3 grid((a.n_ids + per - 1) / per);
+    const uint32_t per = 8;                                        // (id, column block) items per workgroup
+    const uint64_t items = (uint64_t)a.n_ids * Shape(a.M, a.K, 2).CB;
+    const dim3 grid((uint32_t)((items + per - 1) / per));
     if (elem_t == kElemFp8) hipLaunchKernelGGL(k_gather2<kElemFp8>, grid, dim3(256), 0, st, a);
     else hipLaunchKernelGGL(k_gather2<kElemBf16>, grid, dim3(256), 0, st, a);
     return (int)hipGetLastError();

@@ -864,14 +864,15 @@ __global__ void __launch_bounds__(256) k_gather0(GatherArgs a) {
     stage_lut<kLutWindow>(s, a.lut);
     const uint32_t L = threadIdx.x & 31, hw = threadIdx.x >> 5;
     uint32_t *slot = dyn + hw * a.slot_words;
-    const uint32_t id = blockIdx.x * (blockDim.x >> 5) + hw;
+    const Shape f(a.M, a.K, 0);
+    // one half-wave per (id, column block): the blocks of a row decode in parallel
+    const uint32_t item = blockIdx.x * (blockDim.x >> 5) + hw, id = item / f.CB, cb = item - id * f.CB;
     if (id >= a.n_ids) return;
     const int64_t R = a.ids[id];
     if (R < 0 || R >= (int64_t)a.M) return;
-    const Shape f(a.M, a.K, 0);
     const uint32_t rb = (uint32_t)R / kRows0, rr = (uint32_t)R % kRows0;
     uint16_t *o = a.out + (uint64_t)id * f.K16;
-    for (uint32_t cb = 0; cb < f.CB; cb++) {
+    {
         const uint32_t b = rb * f.CB + cb, col0 = cb * kCols + L * 16;
         const bool col_ok = col0 < f.K16;
         const LaneSpan sp = lane_span(a.hdr, b, L);
@@ -882,7 +883,6 @@ __global__ void __launch_bounds__(256) k_gather0(GatherArgs a) {
             gather_block0<ELEM>(s, (const uint32_t *)slot + sh + sp.start, raw, rr, o, col0, col_ok);
         else
             gather_block0<ELEM>(s, (const uint32_t *)(a.data + base) + sp.start, raw, rr, o, col0, col_ok);
-        __builtin_amdgcn_wave_barrier();                        // the slot is overwritten by the next block
     }
 }
 
@@ -915,15 +915,16 @@ __global__ void __launch_bounds__(256) k_gather1(GatherArgs a) {
     constexpr uint32_t RB = ELEM == kElemFp8 ? 8u : 16u;
     const uint32_t L = threadIdx.x & 31, r = L >> 2, q = L & 3, hw = threadIdx.x >> 5;
     uint32_t *slot = dyn + hw * a.slot_words;
-    const uint32_t id = blockIdx.x * (blockDim.x >> 5) + hw;
+    const Shape f(a.M, a.K, 1);
+    // one half-wave per (id, column block): the blocks of a row decode in parallel
+    const uint32_t item = blockIdx.x * (blockDim.x >> 5) + hw, id = item / f.CB, cb = item - id * f.CB;
     if (id >= a.n_ids) return;
     const int64_t R = a.ids[id];
     if (R < 0 || R >= (int64_t)a.M) return;
-    const Shape f(a.M, a.K, 1);
     const uint32_t rb = (uint32_t)R / kRows12, rr = (uint32_t)R % kRows12;
     const bool mine = (rr & 7u) == r, upper = rr >= 8;
     uint16_t *o = a.out + (uint64_t)id * f.K16;
-    for (uint32_t cb = 0; cb < f.CB; cb++) {
+    {
         const uint32_t b = rb * f.CB + cb;
         const uint32_t nsc = ((cb == f.CB - 1 ? f.nl : 32u) + 1) / 2;
         const uint8_t *rp = a.low + ((uint64_t)(rb * f.spr + cb * 16) * kLanes + L) * RB;
@@ -934,7 +935,6 @@ __global__ void __launch_bounds__(256) k_gather1(GatherArgs a) {
             gather_block1<ELEM>(s, (const uint32_t *)slot + sh + sp.start, rp, nsc, mine, upper, o, cb, q, f.K16);
         else
             gather_block1<ELEM>(s, (const uint32_t *)(a.data + base) + sp.start, rp, nsc, mine, upper, o, cb, q, f.K16);
-        __builtin_amdgcn_wave_barrier();
     }
 }
 
@@ -1031,8 +1031,9 @@ int launch_prefix(const LaunchPlan &p, int elem_t, int mode, bool xbf16, const B
 }
 
 int launch_gather_prefix(int layout, int elem_t, const GatherArgs &a, hipStream_t st) {
-    const uint32_t per = 8;                                        // ids per 256-thread workgroup (one per half-wave)
-    const dim3 grid((a.n_ids + per - 1) / per);
+    const uint32_t per = 8;                                        // (id, column block) items per 256-thread workgroup
+    const uint64_t items = (uint64_t)a.n_ids * Shape(a.M, a.K, layout).CB;
+    const dim3 grid((uint32_t)((items + per - 1) / per));
     const size_t lds = (size_t)per * a.slot_words * 4;
     if (layout == 0) {
         if (elem_t == kElemFp8) hipLaunchKernelGGL(k_gather0<kElemFp8>, grid, dim3(256), lds, st, a);
