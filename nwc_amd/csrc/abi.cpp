@@ -55,7 +55,7 @@ constexpr uint32_t kDynLds13 = 47u * 1024u;
 
 bool plan_layout0_tiers(const Shape &f, int mode, int ncu, bool index, uint32_t budget, bool single_only, LaunchPlan &p);
 bool plan_layout0(const Shape &f, int mode, int ncu, bool index, bool seq, LaunchPlan &p) {
-    if (seq && mode == kToken && plan_layout0_tiers(f, mode, ncu, index, kDynLds13, true, p)) {
+    if (seq && (mode == kToken || mode == kDequant) && plan_layout0_tiers(f, mode, ncu, index, kDynLds13, true, p)) {
         p.seq13 = true;
         return true;
     }
@@ -261,6 +261,14 @@ extern "C" int nwc_dequant(void *stream, const uint8_t *data, const uint32_t *ba
                            const uint8_t *low, uint16_t *out, uint64_t n, uint32_t block, uint32_t K, int elem) {
     if (!shape_ok(n, block, K, elem)) return -1;
     return run_blocks(kDequant, true, (hipStream_t)stream, data, bases, hdr, tab, low, nullptr, nullptr, nullptr, out, n, K, elem);
+}
+
+extern "C" int nwc_dequant_seq(void *stream, const uint8_t *data, const uint32_t *bases, const uint8_t *hdr,
+                               const uint32_t *tab, const uint8_t *low, const uint32_t *seq_table, uint16_t *out,
+                               uint64_t n, uint32_t K, int elem) {
+    if (!shape_ok(n, kBlock, K, elem)) return -1;
+    return run_blocks(kDequant, true, (hipStream_t)stream, data, bases, hdr, tab, low, nullptr, nullptr, nullptr, out, n, K,
+                      elem, nullptr, elem_layout(elem) == 0 ? seq_table : nullptr);
 }
 
 extern "C" int nwc_linear_bf16(void *stream, const uint8_t *data, const uint32_t *bases, const uint8_t *hdr, const uint32_t *tab,

@@ -989,9 +989,11 @@ static int launch_layout1s(const LaunchPlan &p, const BlockArgs &a, hipStream_t 
 
 template <int ELEM, int MODE, bool XBF16>
 static int launch_prefix_t(const LaunchPlan &p, const BlockArgs &a, hipStream_t st) {
-    if (p.layout == 0 && p.pipe)
+    if (p.layout == 0 && p.pipe) {
         hipLaunchKernelGGL((k_layout0<ELEM, MODE, XBF16, true, 8>), dim3(p.grid), dim3(p.threads), p.lds, st, a);
-    if constexpr (MODE == kToken && XBF16) {
+        return (int)hipGetLastError();
+    }
+    if constexpr ((MODE == kToken && XBF16) || MODE == kDequant) {
         if (p.layout == 0 && p.seq13 && !p.pipe) {
             if (p.split == 2)
                 hipLaunchKernelGGL((k_layout0<ELEM, MODE, XBF16, false, 4, kPeekSeq>), dim3(p.grid), dim3(p.threads), p.lds, st, a);

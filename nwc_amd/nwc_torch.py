@@ -59,6 +59,8 @@ _lib.nwc_linear_bf16.restype = I32
 _lib.nwc_linear_bf16.argtypes = [P, P, P, P, P, P, P, P, P, P, P, U64, U32, U32, I32]
 _lib.nwc_linear_xbf16.restype = I32
 _lib.nwc_linear_xbf16.argtypes = [P, P, P, P, P, P, P, P, P, P, P, P, U64, U32, I32]
+_lib.nwc_dequant_seq.restype = I32
+_lib.nwc_dequant_seq.argtypes = [P, P, P, P, P, P, P, P, U64, U32, I32]
 _lib.nwc_seq_table.restype = I32
 _lib.nwc_seq_table.argtypes = [P, I32, P]
 _lib.nwc_row_index.restype = I32; _lib.nwc_row_index.argtypes = [P, P, P, P, P, P, P, U64, U32, I32]
@@ -351,8 +353,13 @@ class NWCWeight:
         `out` may supply a preallocated BF16 [out_features, K16] buffer (prefill keeps one per shape)."""
         _need_gpu(self.data)
         w = out if out is not None else torch.empty((self.out_features, self.K16), dtype=torch.bfloat16, device=self.data.device)
-        err = _lib.nwc_dequant(_stream(), _ptr(self.data), _ptr(self.bases), _ptr(self.hdr), _ptr(self.lut),
-                               _ptr(self.low), _ptr(w), self.n, self.block, self.in_features, self.code)
+        st = self.seq_table() if self.layout == 0 else None
+        if st is not None:
+            err = _lib.nwc_dequant_seq(_stream(), _ptr(self.data), _ptr(self.bases), _ptr(self.hdr), _ptr(self.lut),
+                                       _ptr(self.low), _ptr(st), _ptr(w), self.n, self.in_features, self.code)
+        else:
+            err = _lib.nwc_dequant(_stream(), _ptr(self.data), _ptr(self.bases), _ptr(self.hdr), _ptr(self.lut),
+                                   _ptr(self.low), _ptr(w), self.n, self.block, self.in_features, self.code)
         if err:
             raise RuntimeError(f"nwc_dequant HIP error {err}")
         return w if self.K16 == self.in_features else w[:, :self.in_features]

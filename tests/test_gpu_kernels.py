@@ -306,3 +306,40 @@ def test_layout2_split_token_path(cuda, M, K, escapes):
     assert np.all(np.abs(y - y64) <= 2.0 ** -8 * np.abs(y64) + 1e-5)
     y32 = c.matvec(x.float().cuda()).double().cpu().numpy()       # fp32 path: the whole-block kernel
     assert np.all(np.abs(y - y32) <= 2.0 ** -8 * np.abs(y32) + 1e-5)
+
+
+@pytest.mark.parametrize("layout,M,K,escapes", [
+    (0, 64, 20000, "none"), (0, 1003, 1100, "heavy"), (0, 19456, 2560, "none"), (0, 2560, 9728, "heavy"),
+    (1, 64, 20000, "none"), (1, 1003, 1100, "heavy"), (2, 1003, 1100, "none")])
+def test_dequant_with_and_without_table(cuda, layout, M, K, escapes):
+    """nwc_dequant and nwc_dequant_seq (layout 0's 13-bit decode table; layouts 1/2 ignore it) both return the
+    original BF16 bits: a matrix wider than one round of blocks (K = 20000: 40 column blocks, the two-buffer kernel),
+    gate_up and down of Qwen3-4B, and escape rows whose streams exceed their LDS region.  The token path on the wide
+    matrix (one launch of the two-buffer kernel) against float64."""
+    from nwc_amd.nwc_torch import _lib, _ptr, _stream
+    NWCWeight, _, _ = _nwc()
+    print(f"dequant layout {layout} {M}x{K} {escapes}", flush=True)
+    w = bf16_matrix(M, K, seed=M + K, escapes=False)
+    if escapes == "heavy":
+        sign = torch.randint(0, 2, (24, K), generator=torch.Generator().manual_seed(5)) * 2 - 1
+        w[0:24] = (sign * 1e30).to(torch.bfloat16)
+    c = NWCWeight(w, device="cuda", layout=layout)
+    st = c.seq_table() if layout <= 1 else None
+    outs = []
+    for seq in (False, True):
+        out = torch.full((M, c.K16), -1, dtype=torch.int16, device="cuda")
+        if seq:
+            err = _lib.nwc_dequant_seq(_stream(), _ptr(c.data), _ptr(c.bases), _ptr(c.hdr), _ptr(c.lut), _ptr(c.low),
+                                       _ptr(st) if st is not None else None, _ptr(out), c.n, K, c.code)
+        else:
+            err = _lib.nwc_dequant(_stream(), _ptr(c.data), _ptr(c.bases), _ptr(c.hdr), _ptr(c.lut), _ptr(c.low),
+                                   _ptr(out), c.n, c.block, K, c.code)
+        assert err == 0
+        outs.append(out[:, :K].cpu())
+    for o in outs:
+        assert torch.equal(o, w.view(torch.int16))
+    if K > 16384:
+        x = torch.randn(K, generator=torch.Generator().manual_seed(3)).to(torch.bfloat16)
+        y = c.linear_bf16(x.cuda(), None).double().cpu().numpy()
+        y64 = (w.double() @ x.double()).numpy()
+        assert np.all(np.abs(y - y64) <= 2.0 ** -8 * np.abs(y64) + 1e-5)
