@@ -138,18 +138,19 @@ __device__ __forceinline__ Region region_of(const BlockArgs &a, uint32_t b_lo, u
     return r;
 }
 
-// Four 16-byte chunks per thread cover a region buffer of up to 512 words per half-wave.  Lanes past the region
-// re-read its last chunk, so the load count is fixed; native vectors keep the words in registers.
+// Four 16-byte chunks per thread cover a region buffer of up to 512 words per half-wave; native vectors keep the
+// words in registers.  Only chunks inside the region are requested (a wave wholly past it issues nothing): the
+// prologue's vector-memory instructions all pass through the CU's address unit, so a workgroup that requested its
+// full four chunks per thread would delay the other workgroup on its CU (o_proj: 9.3 -> 8.7 us).
 struct Bulk {
     u32x4_t v0, v1, v2, v3;
 };
 __device__ __forceinline__ void bulk_issue(Bulk &B, const uint8_t *__restrict__ data, const Region &r, uint32_t tid, uint32_t nth) {
     const uint8_t *p = data + r.lo16;
-    const uint32_t last = r.n16 - 1u;
-    B.v0 = *(const u32x4_t *)(p + 16u * min(tid, last));
-    B.v1 = *(const u32x4_t *)(p + 16u * min(tid + nth, last));
-    B.v2 = *(const u32x4_t *)(p + 16u * min(tid + 2u * nth, last));
-    B.v3 = *(const u32x4_t *)(p + 16u * min(tid + 3u * nth, last));
+    if (tid < r.n16) B.v0 = *(const u32x4_t *)(p + 16u * tid);
+    if (tid + nth < r.n16) B.v1 = *(const u32x4_t *)(p + 16u * (tid + nth));
+    if (tid + 2u * nth < r.n16) B.v2 = *(const u32x4_t *)(p + 16u * (tid + 2u * nth));
+    if (tid + 3u * nth < r.n16) B.v3 = *(const u32x4_t *)(p + 16u * (tid + 3u * nth));
 }
 __device__ __forceinline__ void bulk_commit(const Bulk &B, uint32_t *buf, const Region &r, uint32_t tid, uint32_t nth) {
     if (tid < r.n16) *(u32x4_t *)(buf + 4u * tid) = B.v0;
