@@ -327,6 +327,234 @@ def run_prefill(args):
             "per_layer": rows, "data": "synthetic N(0,0.02^2) BF16 weights, N(0,1) activations"}
 
 
+# Qwen3 architectures of the BASELINE configs (config.json of Qwen/Qwen3-0.6B and Qwen/Qwen3-4B), built with random
+# N(0, 0.02^2) weights (transformers' default init) since no checkpoint can be fetched here
+QWEN3_ARCH = {
+    "qwen3-0.6b": dict(hidden_size=1024, intermediate_size=3072, num_hidden_layers=28, num_attention_heads=16),
+    "qwen3-4b": dict(hidden_size=2560, intermediate_size=9728, num_hidden_layers=36, num_attention_heads=32),
+}
+
+
+def contiguous_attention(module, query, key, value, attention_mask, scaling=None, dropout=0.0, **kwargs):
+    """Attention for the decode benchmark: fp32 scores and softmax from contiguous operands (grouped KV heads repeated,
+    keys transposed into a copy) under transformers' boolean SDPA mask (None: SDPA's top-left causal).  It keeps every batched
+    product's right operand contiguous, which the BF16 batched GEMMs of this ROCm build need, and creates no tensor
+    from host data, so a token step can be captured as a HIP graph; same maths as eager attention."""
+    import torch
+    rep = query.shape[1] // key.shape[1]
+    k = key.repeat_interleave(rep, dim=1) if rep > 1 else key
+    v = value.repeat_interleave(rep, dim=1) if rep > 1 else value
+    s = torch.matmul(query.float().contiguous(), k.transpose(2, 3).float().contiguous()) * scaling
+    q_len, kv_len = s.shape[-2], s.shape[-1]
+    if attention_mask is not None:
+        m = attention_mask[:, :, :, :kv_len]
+        s = s.masked_fill(~m, float("-inf")) if m.dtype == torch.bool else s + m.float()
+    elif q_len > 1:                                # SDPA's is_causal: query i sees keys 0..i (top-left aligned)
+        s = s.masked_fill(torch.ones(q_len, kv_len, dtype=torch.bool, device=s.device).triu(1), float("-inf"))
+    o = torch.matmul(torch.softmax(s, dim=-1), v.float().contiguous()).to(query.dtype)
+    return o.transpose(1, 2).contiguous(), None
+
+
+def register_attention():
+    from transformers import AttentionInterface
+    from transformers.masking_utils import ALL_MASK_ATTENTION_FUNCTIONS
+    AttentionInterface.register("nwc_contiguous", contiguous_attention)
+    ALL_MASK_ATTENTION_FUNCTIONS.register("nwc_contiguous", ALL_MASK_ATTENTION_FUNCTIONS["sdpa"])
+    return "nwc_contiguous"
+
+
+def qwen3_model(cfg_kw, seed=0, device="cuda"):
+    """A random-init Qwen3ForCausalLM in BF16 on `device` (tied embeddings, head_dim 128, 8 KV heads, 151936 tokens
+    unless cfg_kw says otherwise)."""
+    import torch
+    from transformers import Qwen3Config, Qwen3ForCausalLM
+    kw = dict(vocab_size=151936, head_dim=128, num_key_value_heads=8, tie_word_embeddings=True, rms_norm_eps=1e-6,
+              rope_theta=1000000.0, max_position_embeddings=40960)
+    kw.update(cfg_kw)
+    cfg = Qwen3Config(**kw)
+    cfg._attn_implementation = register_attention()
+    torch.manual_seed(seed)
+    with torch.device(device):
+        model = Qwen3ForCausalLM(cfg).to(torch.bfloat16)
+    return model.eval()
+
+
+def greedy_token(lg, width=128):
+    """First index of the maximum of a 1-D tensor, as torch.argmax, through per-row maxima over rows of `width`
+    elements and an argmax over those: every reduction stays inside one workgroup.  A single argmax over a 151936-entry
+    vocabulary is a multi-workgroup reduction whose zero-initialised counters a captured HIP graph does not reset
+    correctly on later replays."""
+    import torch
+    import torch.nn.functional as F
+    n = lg.numel()
+    rows = F.pad(lg, (0, (-n) % width), value=float("-inf")).view(-1, width)
+    vals, idx = rows.max(dim=1)                         # first maximum of each row
+    r = vals.argmax(dim=0, keepdim=True)                # first row holding the overall maximum
+    return r * width + idx.gather(0, r)
+
+
+class GraphDecoder:
+    """Batch-1 greedy decode with a static KV cache, one token step captured as a HIP graph and replayed (the
+    reference's scripts/graph_decode.py:33-67).  `logits` holds the last step's logits (fp32)."""
+
+    def __init__(self, model, ids, max_new):
+        import torch
+        from transformers import StaticCache
+        self.model, self.ids, self.L = model, ids, ids.shape[1]
+        dev = ids.device
+        self.cache = StaticCache(config=model.config, max_cache_len=self.L + max_new + 8)
+        self.cur = torch.zeros(1, 1, dtype=torch.long, device=dev)
+        self.pos = torch.zeros(1, dtype=torch.long, device=dev)
+        self.res = torch.zeros(max_new + 1, dtype=torch.long, device=dev)
+        self.logits = torch.zeros(model.config.vocab_size, dtype=torch.float32, device=dev)
+        self.graph = None
+
+    def prefill(self):
+        import torch
+        with torch.no_grad():
+            self.cache.reset()
+            out = self.model(input_ids=self.ids, past_key_values=self.cache, use_cache=True,
+                             cache_position=torch.arange(self.L, device=self.ids.device))
+            lg = out.logits[0, -1].float()
+        self.logits.copy_(lg)
+        self.cur.copy_(lg.argmax(-1).view(1, 1))
+        self.pos.fill_(self.L)
+        self.res.zero_()
+        self.res[0] = self.cur[0, 0]
+
+    def step(self):
+        import torch
+        with torch.no_grad():
+            o = self.model(input_ids=self.cur, past_key_values=self.cache, cache_position=self.pos, use_cache=True)
+            lg = o.logits[0, -1].float()
+            self.logits.copy_(lg)
+            nxt = greedy_token(lg)
+            self.pos.add_(1)
+            self.res.index_copy_(0, self.pos - self.L, nxt)
+            self.cur.copy_(nxt.view(1, 1))
+
+    def capture(self):
+        """Warm-up steps on a side stream (lazy per-matrix set-up runs there), then the capture; the cache is left
+        partly written, so call prefill() before replaying."""
+        import torch
+        self.prefill()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            for _ in range(3):
+                self.step()
+        torch.cuda.current_stream().wait_stream(s)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self.step()
+
+
+def compressed_weights_equal(model, orig):
+    """(matrices checked, matrices whose decompressed weights differ from `orig` in any bit): every NWCLinear,
+    NWCEmbedding and fused-projection slice of a converted model against the BF16 state dict taken before conversion."""
+    import torch
+    from nwc_amd.nwc_torch import NWCEmbedding, NWCLinear, _FusedHead
+    checked = bad = 0
+    last = (None, None)
+    for name, m in model.named_modules():
+        if isinstance(m, _FusedHead):
+            lin = m.g["lin"]
+            if last[0] is not lin:
+                last = (lin, lin.w.dequant()[:, :lin.in_features])
+            w = last[1][m.start:m.end]
+        elif isinstance(m, (NWCLinear, NWCEmbedding)):
+            w = m.w.dequant()[:, :m.w.in_features]
+        else:
+            continue
+        ref = orig.get(name + ".weight")
+        if ref is None:
+            continue
+        checked += 1
+        bad += int(not torch.equal(w.view(torch.int16), ref.to(w.device).view(torch.int16)))
+    return checked, bad
+
+
+def run_decode(args):
+    """Model-level batch-1 decode (the caller above the path): a random-init Qwen3 of the config, greedy tokens from a
+    seeded prompt, each token step replayed as one HIP graph; BF16 (hipBLASLt linears) first, then the same model after
+    fuse + convert (NWC lossless, layout 0).  Also checks that graph replays reproduce eager steps bit for bit."""
+    import torch
+    from nwc_amd.nwc_torch import convert, fuse
+    torch.backends.cuda.preferred_blas_library("hipblaslt")
+    name = args.config if args.config in QWEN3_ARCH else "qwen3-4b"
+    dev = torch.device("cuda:0")
+    T, C = args.decode, 16
+    t0 = time.time()
+    model = qwen3_model(QWEN3_ARCH[name], seed=0, device=dev)
+    log(f"decode: random-init {name} built in {time.time() - t0:.1f} s")
+    ids = torch.randint(0, model.config.vocab_size, (1, 16), generator=torch.Generator().manual_seed(7)).to(dev)
+    res = {}
+    for mode in ("bf16", "nwc"):
+        if mode == "nwc":
+            orig = {k: v.detach().cpu().clone() for k, v in model.state_dict().items()
+                    if v.dtype == torch.bfloat16 and v.dim() == 2}
+            t0 = time.time()
+            fuse(model, device=dev)
+            nwc_bytes, bf16_bytes = convert(model, device=dev, verbose=False)
+            torch.cuda.synchronize()
+            log(f"decode: fuse + convert in {time.time() - t0:.1f} s, {nwc_bytes / 1e9:.2f} GB compressed of "
+                f"{bf16_bytes / 1e9:.2f} GB BF16")
+            checked, bad = compressed_weights_equal(model, orig)
+            del orig
+            log(f"decode: {checked} decompressed matrices checked against the BF16 weights, {bad} differ")
+        d = GraphDecoder(model, ids, T + C)
+        # eager reference of the first C steps
+        d.prefill()
+        prefill_logits = d.logits.clone()
+        eager = []
+        for _ in range(C):
+            d.step()
+            eager.append(d.logits.clone())
+        eager_tokens = d.res[: C + 1].clone()
+        d.capture()
+        d.prefill()
+        same = 0
+        for i in range(C):                                 # replays with host work and a sync between them
+            d.graph.replay()
+            torch.cuda.synchronize()
+            same += int(torch.equal(d.logits, eager[i]))
+        tokens_ok = bool(torch.equal(d.res[: C + 1], eager_tokens))
+        log(f"decode {mode}: {same}/{C} graph replays equal to eager steps, tokens equal {tokens_ok}")
+        d.prefill()
+        torch.cuda.synchronize()
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        w0 = time.time()
+        ev0.record()
+        for _ in range(T):
+            d.graph.replay()
+        ev1.record()
+        torch.cuda.synchronize()
+        wall = time.time() - w0
+        ms = ev0.elapsed_time(ev1) / T
+        res[mode] = {"ms_per_token": round(ms, 4), "tokens_per_s": round(1e3 / ms, 1),
+                     "wall_tokens_per_s": round(T / wall, 1), "graph_replays_equal_eager": f"{same}/{C}",
+                     "tokens_equal_eager": tokens_ok, "first_logits": eager[0], "prefill_logits": prefill_logits}
+        log(f"decode {mode}: {ms:.3f} ms/token ({1e3 / ms:.1f} tokens/s)")
+        del d
+        torch.cuda.empty_cache()
+    def rel(key):
+        a, b = res["nwc"][key], res["bf16"][key]
+        return {"max_abs_diff": round(float((a - b).abs().max()), 5), "max_abs": round(float(b.abs().max()), 3),
+                "same_argmax": int(a.argmax()) == int(b.argmax())}
+    cmp = {"prefill (dequant + hipBLASLt GEMM)": rel("prefill_logits"), "first token step (fused matvecs)": rel("first_logits")}
+    for r in res.values():
+        del r["first_logits"], r["prefill_logits"]
+    a = QWEN3_ARCH[name]
+    return {"metric": f"batch-1 greedy decode, random-init {name}, one HIP graph per token", "value": res["nwc"]["tokens_per_s"],
+            "unit": "tokens/s", "higher_is_better": True, "dtype": "bf16",
+            "config": {"workload": f"{name} ({a['num_hidden_layers']} layers, hidden {a['hidden_size']}), 16-token "
+                                   f"seeded prompt, {T} tokens timed", "layout": 0},
+            "bf16_hipblaslt": res["bf16"], "nwc": res["nwc"],
+            "speedup_vs_bf16": round(res["bf16"]["ms_per_token"] / res["nwc"]["ms_per_token"], 3),
+            "weights_bit_exact": {"matrices": checked, "differing": bad}, "logits_vs_bf16": cmp,
+            "data": "random-init N(0,0.02^2) BF16 weights (transformers init), seeded random prompt"}
+
+
 def run_gather(args):
     """configs[4] embedding: --gather seeded uniform ids from the 152064 x 3584 table, per layout; 16 id sets rotate."""
     import torch
@@ -435,6 +663,8 @@ def main():
     ap.add_argument("--config", default="qwen3-4b", choices=sorted(CONFIGS))
     ap.add_argument("--prefill", type=int, default=0, help="time the prefill path for this many tokens instead")
     ap.add_argument("--gather", type=int, default=0, help="time the embedding gather of this many ids instead")
+    ap.add_argument("--decode", type=int, default=0,
+                    help="model-level decode of a random-init Qwen3 (--config qwen3-4b or qwen3-0.6b): this many tokens")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -446,6 +676,9 @@ def main():
         return
     if args.prefill or args.gather:
         print(json.dumps(run_prefill(args) if args.prefill else run_gather(args)), flush=True)
+        return
+    if args.decode:
+        print(json.dumps(run_decode(args)), flush=True)
         return
 
     layers, shapes, elem, layout0, workload = CONFIGS[args.config]
