@@ -336,22 +336,24 @@ QWEN3_ARCH = {
 
 
 def contiguous_attention(module, query, key, value, attention_mask, scaling=None, dropout=0.0, **kwargs):
-    """Attention for the decode benchmark: fp32 scores and softmax from contiguous operands (grouped KV heads repeated,
-    keys transposed into a copy) under transformers' boolean SDPA mask (None: SDPA's top-left causal).  It keeps every batched
-    product's right operand contiguous, which the BF16 batched GEMMs of this ROCm build need, and creates no tensor
-    from host data, so a token step can be captured as a HIP graph; same maths as eager attention."""
+    """Attention for the decode benchmark, with the precision of transformers' eager path (BF16 products with fp32
+    accumulation, fp32 softmax) under its boolean SDPA mask (None: SDPA's top-left causal).  The query heads that
+    share a KV head are stacked as rows of one product, so the cache is not repeated; every batched product's right
+    operand is contiguous (the keys are transposed into a copy), which the BF16 batched GEMMs of this ROCm build need,
+    and no tensor is created from host data, so a token step can be captured as a HIP graph."""
     import torch
-    rep = query.shape[1] // key.shape[1]
-    k = key.repeat_interleave(rep, dim=1) if rep > 1 else key
-    v = value.repeat_interleave(rep, dim=1) if rep > 1 else value
-    s = torch.matmul(query.float().contiguous(), k.transpose(2, 3).float().contiguous()) * scaling
-    q_len, kv_len = s.shape[-2], s.shape[-1]
+    B, H, q_len, D = query.shape
+    hkv = key.shape[1]
+    qg = query.contiguous().view(B, hkv, (H // hkv) * q_len, D)
+    s = torch.matmul(qg, key.transpose(2, 3).contiguous()).float().view(B, H, q_len, -1) * scaling
+    kv_len = s.shape[-1]
     if attention_mask is not None:
         m = attention_mask[:, :, :, :kv_len]
         s = s.masked_fill(~m, float("-inf")) if m.dtype == torch.bool else s + m.float()
     elif q_len > 1:                                # SDPA's is_causal: query i sees keys 0..i (top-left aligned)
         s = s.masked_fill(torch.ones(q_len, kv_len, dtype=torch.bool, device=s.device).triu(1), float("-inf"))
-    o = torch.matmul(torch.softmax(s, dim=-1), v.float().contiguous()).to(query.dtype)
+    p = torch.softmax(s, dim=-1).to(value.dtype).view(B, hkv, -1, kv_len)
+    o = torch.matmul(p, value.contiguous()).view(B, H, q_len, D)
     return o.transpose(1, 2).contiguous(), None
 
 
