@@ -132,7 +132,8 @@ constexpr uint32_t kDynLdsOne = 128u * 1024u;         // dynamic LDS of a workgr
 constexpr uint32_t kDynLdsOne13 = 126u * 1024u;       // the same next to the 13-bit table
 bool plan_layout1_budget(const Shape &f, int mode, int ncu, bool index, uint32_t budget, uint32_t one, LaunchPlan &p);
 bool plan_layout1(const Shape &f, int mode, int ncu, bool index, bool seq, LaunchPlan &p) {
-    if (seq && mode == kToken && index && plan_layout1_budget(f, mode, ncu, index, kDynLds13, kDynLdsOne13, p)) {
+    if (seq && ((mode == kToken && index) || mode == kDequant) &&
+        plan_layout1_budget(f, mode, ncu, index, kDynLds13, kDynLdsOne13, p)) {
         p.seq13 = true;
         return true;
     }
@@ -145,7 +146,7 @@ bool plan_layout1_budget(const Shape &f, int mode, int ncu, bool index, uint32_t
     const uint32_t CB = f.CB, groups = f.groups();
     const uint32_t G = std::max(1u, (groups + 2u * (uint32_t)ncu - 1u) / (2u * (uint32_t)ncu)), blocks = G * CB;
     for (uint32_t sp : {4u, 2u, 1u}) {
-        if (sp > 1 ? !(index && rows) : mode != kRowIndex) continue;
+        if (sp > 1 ? !(index && rows) : (mode != kRowIndex && !(mode == kDequant && budget == kDynLds13))) continue;
         const uint32_t halves = (blocks * sp + 1u) & ~1u;
         if (halves > 32u) continue;
         const uint32_t part = rows ? G * kRows12 * CB * sp * 4u + (f.K16 + 31u) / 32u * 64u : 0u;   // + x as BF16
@@ -272,7 +273,7 @@ extern "C" int nwc_dequant_seq(void *stream, const uint8_t *data, const uint32_t
                                uint64_t n, uint32_t K, int elem) {
     if (!shape_ok(n, kBlock, K, elem)) return -1;
     return run_blocks(kDequant, true, (hipStream_t)stream, data, bases, hdr, tab, low, nullptr, nullptr, nullptr, out, n, K,
-                      elem, nullptr, elem_layout(elem) == 0 ? seq_table : nullptr);
+                      elem, nullptr, elem_layout(elem) <= 1 ? seq_table : nullptr);
 }
 
 extern "C" int nwc_linear_bf16(void *stream, const uint8_t *data, const uint32_t *bases, const uint8_t *hdr, const uint32_t *tab,

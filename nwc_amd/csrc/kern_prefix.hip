@@ -663,6 +663,7 @@ __device__ __forceinline__ float2 chunks1_global(const Tab &s, const uint32_t *l
             ((uint16_t *)a.out)[((uint64_t)c.b * kRowIndexSplits + (sc >> 2) - 1) * kLanes + L] = (uint16_t)S.position(lane);
         const uint4 cw = MODE == kRowIndex ? make_uint4(0u, 0u, 0u, 0u) : raw1<ELEM>(a.low, c, sc);
         const uint4 xc = MODE == kToken || MODE == kF32 ? xs[(kc0 + sc * 32u) >> 3] : make_uint4(0u, 0u, 0u, 0u);
+        uint32_t pa[4], pb[4];
 #pragma unroll
         for (int k = 0; k < 4; k++) {
             const uint32_t s0 = S.s;
@@ -674,10 +675,23 @@ __device__ __forceinline__ float2 chunks1_global(const Tab &s, const uint32_t *l
                 S.reload();
                 S.slow_quad(s, e1, e2);
             }
+            const uint32_t rk = u4_get(cw, k);
             if (MODE == kToken || MODE == kF32) {
-                const uint32_t rk = u4_get(cw, k), xk = u4_get(xc, k);
+                const uint32_t xk = u4_get(xc, k);
                 accA = dot2_bf16(perm(e1, rk, kSelPair0), xk, accA);
                 accB = dot2_bf16(perm(e2, rk, kSelPair2), xk, accB);
+            } else if (MODE == kDequant) {
+                pa[k] = perm(e1, rk, kSelPair0);
+                pb[k] = perm(e2, rk, kSelPair2);
+            }
+        }
+        if (MODE == kDequant) {                                 // as in chunks1
+            const Shape f(a.M, a.K, 1);
+            const uint32_t kc = kc0 + sc * 32u, row0 = c.rb * kRows12, r = L >> 2;
+            if (kc < f.K16) {
+                uint16_t *o = (uint16_t *)a.out + (uint64_t)row0 * f.K16 + kc;
+                if (row0 + r < f.M) *(uint4 *)(o + (uint64_t)r * f.K16) = make_uint4(pa[0], pa[1], pa[2], pa[3]);
+                if (row0 + r + 8 < f.M) *(uint4 *)(o + (uint64_t)(r + 8) * f.K16) = make_uint4(pb[0], pb[1], pb[2], pb[3]);
             }
         }
     }
@@ -698,9 +712,9 @@ __global__ void __launch_bounds__(1024) k_layout1s(BlockArgs a) {
     __shared__ LutT<PEEK> s;
     extern __shared__ uint32_t dyn[];
     const uint32_t tid = threadIdx.x, nth = blockDim.x, L = tid & 31;
-    const uint32_t hw = tid >> 5, H = nth >> 5, HB = H / SP;
-    const uint32_t cap = a.slot_words * HB;
+    const uint32_t hw = tid >> 5;
     const Shape f(a.M, a.K, 1);
+    const uint32_t cap = a.slot_words * a.G * f.CB;            // the plan's region: one slot per block of the tile
     const uint32_t n8 = (f.K16 + 31u) / 32u * 4u;               // x: K32 BF16 values, in chunks of eight
     uint32_t *cur = dyn;
     uint4 *xs = (uint4 *)(dyn + cap);
@@ -725,9 +739,15 @@ __global__ void __launch_bounds__(1024) k_layout1s(BlockArgs a) {
 #pragma unroll
     for (int i = 0; i < kRing1; i++) ring[i] = MODE == kRowIndex ? make_uint4(0u, 0u, 0u, 0u) : raw1<ELEM>(a.low, c, sc0 + i);
     // the copy moves four 16-byte chunks per thread (512 words per half-wave); a larger region (one half-wave per
-    // block, as when the row index is built) decodes from global memory
-    const bool fits = R.n16 <= 4u * nth && R.n16 * 4u <= cap;
-    if (fits) bulk_commit(Bk, cur, R, tid, nth);
+    // block, as when the row index is built) decodes from global memory, except for dequantization, which copies the
+    // rest of its region in a second pass
+    const bool fits = (MODE == kDequant || R.n16 <= 4u * nth) && R.n16 * 4u <= cap;
+    if (fits) {
+        bulk_commit(Bk, cur, R, tid, nth);
+        if (MODE == kDequant)
+            for (uint32_t i = tid + 4u * nth; i < R.n16; i += nth)
+                *(u32x4_t *)(cur + 4u * i) = *(const u32x4_t *)(a.data + R.lo16 + 16u * i);
+    }
     __syncthreads();
     if (t < nt) {
         const uint32_t start = half_scan_incl(n, L) - n;
@@ -983,6 +1003,12 @@ static int launch_layout1s(const LaunchPlan &p, const BlockArgs &a, hipStream_t 
         if (p.split != 1) return -1;
         if (full) hipLaunchKernelGGL((k_layout1s<ELEM, MODE, XBF16, 16, true>), g, b, p.lds, st, a);
         else hipLaunchKernelGGL((k_layout1s<ELEM, MODE, XBF16, 16, false>), g, b, p.lds, st, a);
+        return (int)hipGetLastError();
+    }
+    if constexpr (MODE == kDequant) {                          // one half-wave per block, the 13-bit table
+        if (p.split != 1 || !p.seq13) return -1;
+        if (full) hipLaunchKernelGGL((k_layout1s<ELEM, MODE, XBF16, 16, true, kPeekSeq>), g, b, p.lds, st, a);
+        else hipLaunchKernelGGL((k_layout1s<ELEM, MODE, XBF16, 16, false, kPeekSeq>), g, b, p.lds, st, a);
         return (int)hipGetLastError();
     }
     return -1;

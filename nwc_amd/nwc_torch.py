@@ -353,7 +353,7 @@ class NWCWeight:
         `out` may supply a preallocated BF16 [out_features, K16] buffer (prefill keeps one per shape)."""
         _need_gpu(self.data)
         w = out if out is not None else torch.empty((self.out_features, self.K16), dtype=torch.bfloat16, device=self.data.device)
-        st = self.seq_table() if self.layout == 0 else None
+        st = self.seq_table() if self.layout <= 1 else None
         if st is not None:
             err = _lib.nwc_dequant_seq(_stream(), _ptr(self.data), _ptr(self.bases), _ptr(self.hdr), _ptr(self.lut),
                                        _ptr(self.low), _ptr(st), _ptr(w), self.n, self.in_features, self.code)
