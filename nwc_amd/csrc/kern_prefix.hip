@@ -1005,10 +1005,15 @@ static int launch_layout1s(const LaunchPlan &p, const BlockArgs &a, hipStream_t 
         else hipLaunchKernelGGL((k_layout1s<ELEM, MODE, XBF16, 16, false>), g, b, p.lds, st, a);
         return (int)hipGetLastError();
     }
-    if constexpr (MODE == kDequant) {                          // one half-wave per block, the 13-bit table
-        if (p.split != 1 || !p.seq13) return -1;
-        if (full) hipLaunchKernelGGL((k_layout1s<ELEM, MODE, XBF16, 16, true, kPeekSeq>), g, b, p.lds, st, a);
-        else hipLaunchKernelGGL((k_layout1s<ELEM, MODE, XBF16, 16, false, kPeekSeq>), g, b, p.lds, st, a);
+    if constexpr (MODE == kDequant) {                          // one half-wave per block
+        if (p.split != 1) return -1;
+        if (p.seq13) {
+            if (full) hipLaunchKernelGGL((k_layout1s<ELEM, MODE, XBF16, 16, true, kPeekSeq>), g, b, p.lds, st, a);
+            else hipLaunchKernelGGL((k_layout1s<ELEM, MODE, XBF16, 16, false, kPeekSeq>), g, b, p.lds, st, a);
+        } else {
+            if (full) hipLaunchKernelGGL((k_layout1s<ELEM, MODE, XBF16, 16, true>), g, b, p.lds, st, a);
+            else hipLaunchKernelGGL((k_layout1s<ELEM, MODE, XBF16, 16, false>), g, b, p.lds, st, a);
+        }
         return (int)hipGetLastError();
     }
     return -1;
