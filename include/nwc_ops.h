@@ -52,7 +52,7 @@ int nwc_matvec(void *stream, const uint8_t *data, const uint32_t *bases, const u
 int nwc_dequant(void *stream, const uint8_t *data, const uint32_t *bases, const uint8_t *hdr, const uint32_t *tab,
                 const uint8_t *low, uint16_t *out, uint64_t n, uint32_t block, uint32_t K, int elem);
 
-/* nwc_dequant with layout 0's 13-bit decode table from nwc_seq_table (device; NULL, or layouts 1/2: as nwc_dequant),
+/* nwc_dequant with the 13-bit decode table from nwc_seq_table (device; layouts 0/1; NULL, or layout 2: as nwc_dequant),
  * block fixed at 4096: fewer decode steps take the slow path, same output.  No counterpart in the reference. */
 int nwc_dequant_seq(void *stream, const uint8_t *data, const uint32_t *bases, const uint8_t *hdr, const uint32_t *tab,
                     const uint8_t *low, const uint32_t *seq_table, uint16_t *out, uint64_t n, uint32_t K, int elem);
