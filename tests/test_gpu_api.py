@@ -140,3 +140,61 @@ def test_ref_fp8_baseline_module(cuda):
     y64 = ref_matvec64(bits16(q.to(torch.bfloat16)), x.float().cpu().numpy().ravel(), scale=scale.numpy())
     err = np.abs(mod(x).double().cpu().numpy().ravel() - y64)
     assert np.all(err <= 2.0 ** -8 * np.abs(y64) + 1e-5)
+
+
+def test_qwen2_checkpoint_round_trip_with_fp8(cuda, tmp_path):
+    """The reference's tests/test_checkpoint.py flow on its tiny random Qwen2 (vocab 4096, hidden 256, intermediate 1000,
+    2 layers, tied embeddings; projection biases on q/k/v, a down_proj with K = 1000 not a multiple of 16): fuse +
+    convert -> save -> load gives identical logits; export_bf16 gives every original tensor back bit for bit and a
+    model whose logits equal the original's; an fp8 conversion of the exported model reproduces its logits after
+    save -> load (test_checkpoint.py:11-56)."""
+    import nwc_amd
+    from safetensors.torch import load_file
+    from transformers import AutoModelForCausalLM, Qwen2Config
+    print("tiny Qwen2 checkpoint round trip", flush=True)
+    torch.manual_seed(0)
+    cfg = Qwen2Config(vocab_size=4096, hidden_size=256, intermediate_size=1000, num_hidden_layers=2, num_attention_heads=4,
+                      num_key_value_heads=2, max_position_embeddings=512, tie_word_embeddings=True)
+    try:
+        model = AutoModelForCausalLM.from_config(cfg, dtype=torch.bfloat16).eval()
+    except TypeError:
+        model = AutoModelForCausalLM.from_config(cfg, torch_dtype=torch.bfloat16).eval()
+    ids = torch.randint(0, cfg.vocab_size, (1, 12), generator=torch.Generator().manual_seed(1))
+    with torch.no_grad():
+        ref = model(ids).logits.float()                                     # BF16 on the CPU
+    state = {k: v.clone() for k, v in model.state_dict().items()}
+    nwc_amd.fuse(model, device="cuda")
+    nwc_amd.convert(model, device="cuda", verbose=False)
+    with torch.no_grad():
+        a = model(ids.cuda()).logits.float()
+    d = tmp_path / "ckpt"
+    c = nwc_amd.save_pretrained(model, str(d), base_model="test")
+    assert c["bytes_nwc"] < c["bytes_bf16"] and len(c["weights"]) > 0
+    del model
+    m2 = nwc_amd.load_pretrained(str(d), device="cuda", verbose=False)
+    with torch.no_grad():
+        b = m2(ids.cuda()).logits.float()
+    assert torch.equal(a, b)
+    assert (b.cpu() - ref).abs().max() < 0.5
+    assert all(p.device.type == "cuda" for p in m2.parameters())
+    e = tmp_path / "bf16"
+    nwc_amd.export_bf16(str(d), str(e), device="cuda", verbose=False)
+    exported = load_file(str(e / "model.safetensors"))
+    missing = [k for k in state if k not in exported and k != "lm_head.weight"]
+    differ = [k for k in state if k in exported and not torch.equal(exported[k].to(state[k].dtype), state[k])]
+    assert not missing and not differ, (missing[:3], differ[:3])
+    try:
+        m3 = AutoModelForCausalLM.from_pretrained(str(e), dtype=torch.bfloat16).eval()
+    except TypeError:
+        m3 = AutoModelForCausalLM.from_pretrained(str(e), torch_dtype=torch.bfloat16).eval()
+    with torch.no_grad():
+        assert torch.equal(m3(ids).logits.float(), ref)
+    nwc_amd.fuse(m3, device="cuda", elem="fp8")
+    nwc_amd.convert(m3, device="cuda", verbose=False, elem="fp8")
+    with torch.no_grad():
+        a8 = m3(ids.cuda()).logits.float()
+    nwc_amd.save_pretrained(m3, str(tmp_path / "fp8"), base_model="test")
+    del m3
+    m5 = nwc_amd.load_pretrained(str(tmp_path / "fp8"), device="cuda", verbose=False)
+    with torch.no_grad():
+        assert torch.equal(m5(ids.cuda()).logits.float(), a8)
