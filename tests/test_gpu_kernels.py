@@ -343,3 +343,30 @@ def test_dequant_with_and_without_table(cuda, layout, M, K, escapes):
         y = c.linear_bf16(x.cuda(), None).double().cpu().numpy()
         y64 = (w.double() @ x.double()).numpy()
         assert np.all(np.abs(y - y64) <= 2.0 ** -8 * np.abs(y64) + 1e-5)
+
+
+REF_TEST_K_SHAPES = [(8192, 4608), (4096, 11008), (1024, 3600), (2048, 2064), (512, 16384), (19456, 2560), (1024, 9728),
+                     (1001, 1000), (13, 40), (8, 16), (3, 4097)]
+
+
+@pytest.mark.parametrize("layout", LAYOUTS)
+@pytest.mark.parametrize("M,K", REF_TEST_K_SHAPES)
+def test_reference_test_k_shapes(cuda, layout, M, K):
+    """The reference's tests/test_k.py shapes (:10-11: K not a multiple of 512 or 16, M not a multiple of 8), with
+    seeded N(0, 0.02^2) weights instead of its data/W.raw (absent here) and its activations (rand - 0.5) and bias:
+    dequant bit-exact; token path within one BF16 ulp of float64 (the reference accepts 2e-2 against F.linear); fp32
+    path within 1e-3 relative (the reference: 1e-4 relative to |ref| + 1e-2)."""
+    NWCWeight, _, _ = _nwc()
+    print(f"test_k shape layout {layout} {M}x{K}", flush=True)
+    w = bf16_matrix(M, K, seed=M + 3 * K)
+    c = NWCWeight(w, device="cuda", layout=layout)
+    assert torch.equal(c.dequant().cpu().view(torch.int16), w.view(torch.int16))
+    g = torch.Generator().manual_seed(1)
+    xb = (torch.rand(K, generator=g) - 0.5).to(torch.bfloat16)
+    bias = (torch.rand(M, generator=g) - 0.5).to(torch.bfloat16)
+    y = c.linear_bf16(xb.cuda(), bias.cuda())
+    wd = w.cuda().double()
+    y64 = (wd @ xb.cuda().double() + bias.cuda().double()).cpu().numpy()
+    _check_bf16(y, y64, 0.02)
+    y32 = c.matvec(xb.float().cuda()).double().cpu().numpy()
+    _check_f32(y32, (wd @ xb.cuda().double()).cpu().numpy(), 0.02)
