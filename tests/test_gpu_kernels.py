@@ -370,3 +370,25 @@ def test_reference_test_k_shapes(cuda, layout, M, K):
     _check_bf16(y, y64, 0.02)
     y32 = c.matvec(xb.float().cuda()).double().cpu().numpy()
     _check_f32(y32, (wd @ xb.cuda().double()).cpu().numpy(), 0.02)
+
+
+@pytest.mark.parametrize("layout", LAYOUTS)
+@pytest.mark.parametrize("M,K", [(4096, 2560), (8192, 4608), (151936 // 8, 2560), (2048, 2064), (1001, 1000), (13, 40)])
+def test_reference_gather_shapes(cuda, layout, M, K):
+    """The reference's tests/test_gather.py shapes (:12) and ids (64, including 0, M - 1 and M / 2, :18): rows
+    bit-exact; ids outside [0, M) leave their output rows untouched."""
+    NWCWeight, _, _ = _nwc()
+    print(f"gather shape layout {layout} {M}x{K}", flush=True)
+    w = bf16_matrix(M, K, seed=5 * M + K)
+    c = NWCWeight(w, device="cuda", layout=layout)
+    g = torch.Generator().manual_seed(2)
+    ids = torch.cat([torch.tensor([0, M - 1, M // 2]), torch.randint(0, M, (61,), generator=g)])
+    assert torch.equal(c.gather(ids.cuda()).cpu().view(torch.int16), w[ids].view(torch.int16))
+    from nwc_amd.nwc_torch import _lib, _ptr, _stream
+    bad = torch.tensor([-1, M, 0, M + 7], dtype=torch.int64, device="cuda")
+    out = torch.full((4, c.K16), 0x1234, dtype=torch.int16, device="cuda")
+    assert _lib.nwc_gather(_stream(), _ptr(c.data), _ptr(c.bases), _ptr(c.hdr), _ptr(c.lut), _ptr(c.low), _ptr(bad), 4,
+                           _ptr(out), c.n, c.block, K, c.code) == 0
+    out = out.cpu()
+    assert torch.all(out[[0, 1, 3]] == 0x1234)
+    assert torch.equal(out[2, :K], w[0].view(torch.int16))
