@@ -19,7 +19,7 @@ pytestmark = pytest.mark.gpu
 
 SHAPES = [(8, 512, 0.02), (13, 40, 0.02), (3, 4097, 0.02), (100, 1000, 1.0), (64, 2048, 0.02), (17, 520, 0.02),
           (1001, 1000, 0.02), (8, 16, 0.02), (1, 1, 0.02)]
-FP8_SHAPES = [(8, 512), (13, 40), (3, 4097), (1001, 1000), (2560, 4096)]
+FP8_SHAPES = [(8, 512), (13, 40), (3, 4097), (1001, 1000), (2560, 4096), (6144, 2560)]   # tests/test_fp8.py:45
 LAYOUTS = [0, 1, 2]
 
 
