@@ -611,6 +611,53 @@ def run_cpu(args):
             "us_per_matvec": round(dt / reps * 1e6, 1)}
 
 
+def run_encode(args):
+    """Host encoder throughput on BASELINE configs[0] (9728 x 2560 BF16, layout 0): the library's multithreaded
+    nwc_encode against the C oracle's single-threaded restatement of the reference encoder (nwc_ops.cu:245-320, which
+    is single-threaded too), outputs byte-identical.  No GPU needed."""
+    import numpy as np
+    import torch
+    from nwc_amd.nwc_torch import _lib, _ptr, NPAIR, HDR_BLOCK, RAW_SLACK, _layout_info
+    from oracle import oracle as O
+    M, K = 9728, 2560
+    w = make_weight(M, K, 7)
+    src = w.view(torch.int16).contiguous()
+    n = M * K
+    nb, n_low, _, _ = _layout_info(M, K, 0)
+    cap = n + n // 2 + nb * 64 + 4096
+    bufs = dict(freq=torch.empty(NPAIR, dtype=torch.int16), psym=torch.empty(NPAIR, dtype=torch.int16),
+                bases=torch.empty(nb, dtype=torch.int32), hdr=torch.empty(nb * HDR_BLOCK, dtype=torch.uint8),
+                data=torch.empty(cap, dtype=torch.uint8), low=torch.zeros(n_low + RAW_SLACK, dtype=torch.uint8))
+
+    def ours():
+        return _lib.nwc_encode(_ptr(src), n, K, 0, _ptr(bufs["freq"]), _ptr(bufs["psym"]), _ptr(bufs["bases"]),
+                               _ptr(bufs["hdr"]), _ptr(bufs["data"]), cap, _ptr(bufs["low"]))
+    dl = ours()
+    times = []
+    for _ in range(5):
+        t0 = time.perf_counter()
+        ours()
+        times.append(time.perf_counter() - t0)
+    t_ours = statistics.median(times)
+    wn = src.numpy().view(np.uint16)
+    t0 = time.perf_counter()
+    enc = O.encode(wn, 0, 0)
+    t_ref = time.perf_counter() - t0
+    same = (enc["dl"] == dl and np.array_equal(enc["data"][:dl], bufs["data"].numpy()[:dl])
+            and np.array_equal(enc["bases"], bufs["bases"].numpy().view(np.uint32))
+            and np.array_equal(enc["hdr"], bufs["hdr"].numpy()) and np.array_equal(enc["low"], bufs["low"].numpy()))
+    if not same:
+        raise SystemExit("encoder output differs from the oracle's")
+    cores = len(os.sched_getaffinity(0))
+    return {"metric": "host encode throughput, 9728x2560 BF16 layout 0 (BASELINE configs[0])",
+            "value": round(n / t_ours / 1e6, 1), "unit": "M weights/s", "higher_is_better": True,
+            "ms": round(t_ours * 1e3, 2), "byte_identical_to_oracle": same, "cores": cores,
+            "cpu_baseline": {"value": round(n / t_ref / 1e6, 1), "unit": "M weights/s", "cores": 1, "kind": "port",
+                             "ms": round(t_ref * 1e3, 1),
+                             "sample": "the C oracle's single-threaded restatement of the reference encoder, one run"},
+            "speedup": round(t_ref / t_ours, 2)}
+
+
 def traffic_bytes():
     """HBM bytes per gate_up launch from the committed rocprofv3 counter summary (FETCH_SIZE + WRITE_SIZE, each scaled
     by the factor a plain copy of known size gives), or None when there is none."""
@@ -665,6 +712,7 @@ def main():
     ap.add_argument("--config", default="qwen3-4b", choices=sorted(CONFIGS))
     ap.add_argument("--prefill", type=int, default=0, help="time the prefill path for this many tokens instead")
     ap.add_argument("--gather", type=int, default=0, help="time the embedding gather of this many ids instead")
+    ap.add_argument("--encode", action="store_true", help="time the host encoder on configs[0] (no GPU)")
     ap.add_argument("--decode", type=int, default=0,
                     help="model-level decode of a random-init Qwen3 (--config qwen3-4b or qwen3-0.6b): this many tokens")
     args = ap.parse_args()
@@ -681,6 +729,9 @@ def main():
         return
     if args.decode:
         print(json.dumps(run_decode(args)), flush=True)
+        return
+    if args.encode:
+        print(json.dumps(run_encode(args)), flush=True)
         return
 
     layers, shapes, elem, layout0, workload = CONFIGS[args.config]
