@@ -191,16 +191,19 @@ bool plan_blocks(const Shape &f, int layout, int mode, int ncu, bool index, Laun
     p.layout = layout;
     const uint32_t CB = f.CB, groups = f.groups(), slot = slot_words_for(layout);
     // layout 2, BF16 token path, few row groups per CU: four or two half-waves per block (super-chunk ranges), one
-    // round (the token path of layouts 1/2 always takes BF16 x)
+    // round (the token path of layouts 1/2 always takes BF16 x); for wide rows, several such items per half-wave
     if (layout == 2 && !fp8 && mode == kToken) {
         const uint32_t G = std::max(1u, (groups + 2u * (uint32_t)ncu - 1u) / (2u * (uint32_t)ncu));
         for (uint32_t sp : {4u, 2u}) {
             const uint32_t halves = (G * CB * sp + 1u) & ~1u;
             const uint32_t lds = (f.K16 + 31u) / 32u * 64u + G * f.rows * CB * sp * 4u;   // x as BF16, partial sums
-            if (halves > 32u || lds > kDynLdsPipe) continue;
+            // rows of 32 column blocks or more (7B down, 37): two half-waves per block even though the tile's
+            // 2 CB items then exceed 32 half-waves and go round-robin (25.9 -> 23.6 us)
+            const bool wide = CB >= 32u && sp == 2u;
+            if ((halves > 32u && !wide) || lds > kDynLdsPipe) continue;
             p.split = sp;
             p.G = G;
-            p.threads = 32u * halves;
+            p.threads = 32u * std::min(32u, halves);
             p.grid = (groups + G - 1u) / G;
             p.lds = lds;
             return true;
