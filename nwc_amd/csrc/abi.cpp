@@ -190,31 +190,33 @@ bool plan_blocks(const Shape &f, int layout, int mode, int ncu, bool index, Laun
     p = LaunchPlan{};
     p.layout = layout;
     const uint32_t CB = f.CB, groups = f.groups(), slot = slot_words_for(layout);
-    // layout 2, BF16 token path, few row groups per CU: four or two half-waves per block (super-chunk ranges), one
-    // round (the token path of layouts 1/2 always takes BF16 x); for wide rows, several such items per half-wave
+    // layout 2, BF16 token path: G = ceil(groups / (2 CUs)) whole row groups per workgroup, each block's 16
+    // super-chunks split into four (or two) ranges.  With at most 32 ranges per tile, one half-wave each (7B qkv, o);
+    // otherwise four ranges per block go round-robin over 32 half-waves (7B gate_up: 41.2 -> 36.5-36.9 us against one
+    // half-wave per block, down 25.9 -> 23.7).  x is staged in LDS as BF16 (the token path of layouts 1/2 always
+    // takes BF16 x).
     if (layout == 2 && !fp8 && mode == kToken) {
         const uint32_t G = std::max(1u, (groups + 2u * (uint32_t)ncu - 1u) / (2u * (uint32_t)ncu));
-        for (uint32_t sp : {4u, 2u}) {
-            const uint32_t halves = (G * CB * sp + 1u) & ~1u;
-            const uint32_t lds = (f.K16 + 31u) / 32u * 64u + G * f.rows * CB * sp * 4u;   // x as BF16, partial sums
-            // rows of 32 column blocks or more (7B down, 37): two half-waves per block even though the tile's
-            // 2 CB items then exceed 32 half-waves and go round-robin (25.9 -> 23.6 us)
-            const bool wide = CB >= 32u && sp == 2u;
-            if ((halves > 32u && !wide) || lds > kDynLdsPipe) continue;
+        auto lds_sp = [&](uint32_t sp) { return (f.K16 + 31u) / 32u * 64u + G * f.rows * CB * sp * 4u; };
+        auto take = [&](uint32_t sp, uint32_t halves) {
             p.split = sp;
             p.G = G;
-            p.threads = 32u * std::min(32u, halves);
+            p.threads = 32u * halves;
             p.grid = (groups + G - 1u) / G;
-            p.lds = lds;
+            p.lds = lds_sp(sp);
             return true;
+        };
+        for (uint32_t sp : {4u, 2u}) {
+            const uint32_t halves = (G * CB * sp + 1u) & ~1u;
+            if (halves <= 32u && lds_sp(sp) <= kDynLdsPipe) return take(sp, halves);
         }
+        if (lds_sp(4u) <= kDynLdsPipe) return take(4u, 32u);
     }
     uint32_t G = CB >= 32 ? 1u : 32u / CB;
     while (G > 1 && (groups + G - 1) / G < 2u * (uint32_t)ncu) G--;
     if (G > 1 && ((G * CB) & 1u)) G--;
-    // layout 2's single-round token kernel: at most two workgroups per CU even if a tile then holds more blocks than
-    // half-waves (some take two): 7B gate_up has 16576 blocks, just more than 512 workgroups of 32 half-waves hold,
-    // and a second round of 80 workgroups costs more (42.1 -> 40.6 us)
+    // layout 2's token path when the split's partial sums do not fit (whole blocks, one round): at most two
+    // workgroups per CU even if a tile then holds more blocks than half-waves
     if (layout == 2 && !fp8 && mode == kToken && CB < 32u)
         G = std::max(G, (groups + 2u * (uint32_t)ncu - 1u) / (2u * (uint32_t)ncu));
     if (G > groups) G = groups;
