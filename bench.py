@@ -669,7 +669,7 @@ def traffic_bytes():
 
 
 def run_profile(args):
-    """Counter target: --profile-launches launches of one Qwen3-4B matrix (--profile-shape, default gate_up), after
+    """Counter target: --profile-launches launches of one matrix of --config (--profile-shape, default gate_up), after
     three device copies of 256 MiB (the calibration kernel of known size).  Run under rocprofv3 --pmc; prints one line
     per phase."""
     import torch
@@ -682,8 +682,10 @@ def run_profile(args):
     torch.cuda.synchronize()
     print("calibration: 3 copies of 268435456 bytes", flush=True)
     del src, dst
-    name, M, K = next(s for s in SHAPES if s[0] == args.profile_shape)
-    c = NWCWeight(make_weight(M, K, 1000 + [s[0] for s in SHAPES].index(name)), device=dev, layout=args.layout)
+    _, shapes, elem, layout0, _ = CONFIGS[args.config]
+    layout = args.layout if args.config in ("qwen3-4b", "qwen3-4b-fp8") else layout0
+    name, M, K = next(s for s in shapes if s[0] == args.profile_shape)
+    c = NWCWeight(make_weight(M, K, 1000 + [s[0] for s in shapes].index(name)), device=dev, layout=layout, elem=elem)
     cs = [c] + [clone_weight(c) for _ in range(7)]
     x = torch.randn(K, generator=torch.Generator().manual_seed(2)).to(torch.bfloat16).to(dev)
     ys = [torch.empty(M, dtype=torch.bfloat16, device=dev) for _ in cs]
