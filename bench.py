@@ -455,7 +455,8 @@ class GraphDecoder:
 
 def compressed_weights_equal(model, orig):
     """(matrices checked, matrices whose decompressed weights differ from `orig` in any bit): every NWCLinear,
-    NWCEmbedding and fused-projection slice of a converted model against the BF16 state dict taken before conversion."""
+    NWCEmbedding and fused-projection slice of a converted model against the BF16 state dict taken before conversion
+    (fp8 matrices: against quantize_fp8 of it)."""
     import torch
     from nwc_amd.nwc_torch import NWCEmbedding, NWCLinear, _FusedHead
     checked = bad = 0
@@ -473,9 +474,18 @@ def compressed_weights_equal(model, orig):
         ref = orig.get(name + ".weight")
         if ref is None:
             continue
+        ref = ref.to(w.device)
+        if m_elem(m) == "fp8":                          # the stored values are quantize_fp8's codes, unscaled
+            from nwc_amd.nwc_torch import quantize_fp8
+            ref = quantize_fp8(ref)[0].to(torch.bfloat16)
         checked += 1
-        bad += int(not torch.equal(w.view(torch.int16), ref.to(w.device).view(torch.int16)))
+        bad += int(not torch.equal(w.view(torch.int16), ref.view(torch.int16)))
     return checked, bad
+
+
+def m_elem(m):
+    w = m.g["lin"].w if hasattr(m, "g") else m.w
+    return "fp8" if w.scale is not None else "bf16"
 
 
 def run_decode(args):
@@ -498,8 +508,8 @@ def run_decode(args):
             orig = {k: v.detach().cpu().clone() for k, v in model.state_dict().items()
                     if v.dtype == torch.bfloat16 and v.dim() == 2}
             t0 = time.time()
-            fuse(model, device=dev)
-            nwc_bytes, bf16_bytes = convert(model, device=dev, verbose=False)
+            fuse(model, device=dev, elem=args.decode_elem)
+            nwc_bytes, bf16_bytes = convert(model, device=dev, verbose=False, elem=args.decode_elem)
             torch.cuda.synchronize()
             log(f"decode: fuse + convert in {time.time() - t0:.1f} s, {nwc_bytes / 1e9:.2f} GB compressed of "
                 f"{bf16_bytes / 1e9:.2f} GB BF16")
@@ -550,9 +560,9 @@ def run_decode(args):
         del r["first_logits"], r["prefill_logits"]
     a = QWEN3_ARCH[name]
     return {"metric": f"batch-1 greedy decode, random-init {name}, one HIP graph per token", "value": res["nwc"]["tokens_per_s"],
-            "unit": "tokens/s", "higher_is_better": True, "dtype": "bf16",
+            "unit": "tokens/s", "higher_is_better": True, "dtype": args.decode_elem,
             "config": {"workload": f"{name} ({a['num_hidden_layers']} layers, hidden {a['hidden_size']}), 16-token "
-                                   f"seeded prompt, {T} tokens timed", "layout": 0},
+                                   f"seeded prompt, {T} tokens timed", "layout": 0, "nwc_elem": args.decode_elem},
             "bf16_hipblaslt": res["bf16"], "nwc": res["nwc"],
             "speedup_vs_bf16": round(res["bf16"]["ms_per_token"] / res["nwc"]["ms_per_token"], 3),
             "weights_bit_exact": {"matrices": checked, "differing": bad}, "logits_vs_bf16": cmp,
@@ -717,6 +727,8 @@ def main():
     ap.add_argument("--prefill", type=int, default=0, help="time the prefill path for this many tokens instead")
     ap.add_argument("--gather", type=int, default=0, help="time the embedding gather of this many ids instead")
     ap.add_argument("--encode", action="store_true", help="time the host encoder on configs[0] (no GPU)")
+    ap.add_argument("--decode-elem", default="bf16", choices=["bf16", "fp8"],
+                    help="--decode: the NWC model's weights, lossless BF16 or weight-only fp8 (BASELINE configs[3])")
     ap.add_argument("--decode", type=int, default=0,
                     help="model-level decode of a random-init Qwen3 (--config qwen3-4b or qwen3-0.6b): this many tokens")
     args = ap.parse_args()
