@@ -85,7 +85,7 @@ bool plan_layout0_tiers(const Shape &f, int mode, int ncu, bool index, uint32_t 
     // 512 row groups): one, with twice the row groups, then stages its 32 KB decode table for twice the work
     // (Qwen3-0.6B qkv 4096x1024 and gate_up 6144x1024: 11-12% faster)
     const uint32_t wgpc = ceil_div(groups, 2u * ncu_) * CB <= 4u ? 1u : 2u;
-    if (index && rows) {
+    if (index && (rows || mode == kDequant)) {
         const uint32_t G = std::max(1u, ceil_div(groups, wgpc * ncu_)), blocks = G * CB;
         const uint32_t lds = blocks * kSlotWords0 * 4u + G * part;
         if (lds <= budget) {
@@ -279,11 +279,12 @@ extern "C" int nwc_dequant(void *stream, const uint8_t *data, const uint32_t *ba
 }
 
 extern "C" int nwc_dequant_seq(void *stream, const uint8_t *data, const uint32_t *bases, const uint8_t *hdr,
-                               const uint32_t *tab, const uint8_t *low, const uint32_t *seq_table, uint16_t *out,
-                               uint64_t n, uint32_t K, int elem) {
+                               const uint32_t *tab, const uint8_t *low, const uint16_t *row_index,
+                               const uint32_t *seq_table, uint16_t *out, uint64_t n, uint32_t K, int elem) {
     if (!shape_ok(n, kBlock, K, elem)) return -1;
+    const int layout = elem_layout(elem);
     return run_blocks(kDequant, true, (hipStream_t)stream, data, bases, hdr, tab, low, nullptr, nullptr, nullptr, out, n, K,
-                      elem, nullptr, elem_layout(elem) <= 1 ? seq_table : nullptr);
+                      elem, layout == 0 ? row_index : nullptr, layout <= 1 ? seq_table : nullptr);
 }
 
 extern "C" int nwc_linear_bf16(void *stream, const uint8_t *data, const uint32_t *bases, const uint8_t *hdr, const uint32_t *tab,

@@ -60,7 +60,7 @@ _lib.nwc_linear_bf16.argtypes = [P, P, P, P, P, P, P, P, P, P, P, U64, U32, U32,
 _lib.nwc_linear_xbf16.restype = I32
 _lib.nwc_linear_xbf16.argtypes = [P, P, P, P, P, P, P, P, P, P, P, P, U64, U32, I32]
 _lib.nwc_dequant_seq.restype = I32
-_lib.nwc_dequant_seq.argtypes = [P, P, P, P, P, P, P, P, U64, U32, I32]
+_lib.nwc_dequant_seq.argtypes = [P, P, P, P, P, P, P, P, P, U64, U32, I32]
 _lib.nwc_seq_table.restype = I32
 _lib.nwc_seq_table.argtypes = [P, I32, P]
 _lib.nwc_row_index.restype = I32; _lib.nwc_row_index.argtypes = [P, P, P, P, P, P, P, U64, U32, I32]
@@ -355,8 +355,10 @@ class NWCWeight:
         w = out if out is not None else torch.empty((self.out_features, self.K16), dtype=torch.bfloat16, device=self.data.device)
         st = self.seq_table() if self.layout <= 1 else None
         if st is not None:
+            ri = self.row_index() if self.layout == 0 else None
             err = _lib.nwc_dequant_seq(_stream(), _ptr(self.data), _ptr(self.bases), _ptr(self.hdr), _ptr(self.lut),
-                                       _ptr(self.low), _ptr(st), _ptr(w), self.n, self.in_features, self.code)
+                                       _ptr(self.low), _ptr(ri) if ri is not None else None, _ptr(st), _ptr(w), self.n,
+                                       self.in_features, self.code)
         else:
             err = _lib.nwc_dequant(_stream(), _ptr(self.data), _ptr(self.bases), _ptr(self.hdr), _ptr(self.lut),
                                    _ptr(self.low), _ptr(w), self.n, self.block, self.in_features, self.code)

@@ -314,7 +314,7 @@ def test_layout2_split_token_path(cuda, M, K, escapes):
     (0, 64, 20000, "none"), (0, 1003, 1100, "heavy"), (0, 19456, 2560, "none"), (0, 2560, 9728, "heavy"),
     (1, 64, 20000, "none"), (1, 1003, 1100, "heavy"), (2, 1003, 1100, "none")])
 def test_dequant_with_and_without_table(cuda, layout, M, K, escapes):
-    """nwc_dequant and nwc_dequant_seq (layout 0's 13-bit decode table; layouts 1/2 ignore it) both return the
+    """nwc_dequant and nwc_dequant_seq (13-bit decode table for layouts 0/1, row index for layout 0) both return the
     original BF16 bits: a matrix wider than one round of blocks (K = 20000: 40 column blocks, the two-buffer kernel),
     gate_up and down of Qwen3-4B, and escape rows whose streams exceed their LDS region.  The token path on the wide
     matrix (one launch of the two-buffer kernel) against float64."""
@@ -331,8 +331,10 @@ def test_dequant_with_and_without_table(cuda, layout, M, K, escapes):
     for seq in (False, True):
         out = torch.full((M, c.K16), -1, dtype=torch.int16, device="cuda")
         if seq:
+            ri = c.row_index() if layout == 0 else None
             err = _lib.nwc_dequant_seq(_stream(), _ptr(c.data), _ptr(c.bases), _ptr(c.hdr), _ptr(c.lut), _ptr(c.low),
-                                       _ptr(st) if st is not None else None, _ptr(out), c.n, K, c.code)
+                                       _ptr(ri) if ri is not None else None, _ptr(st) if st is not None else None,
+                                       _ptr(out), c.n, K, c.code)
         else:
             err = _lib.nwc_dequant(_stream(), _ptr(c.data), _ptr(c.bases), _ptr(c.hdr), _ptr(c.lut), _ptr(c.low),
                                    _ptr(out), c.n, c.block, K, c.code)
