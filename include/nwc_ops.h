@@ -52,9 +52,9 @@ int nwc_matvec(void *stream, const uint8_t *data, const uint32_t *bases, const u
 int nwc_dequant(void *stream, const uint8_t *data, const uint32_t *bases, const uint8_t *hdr, const uint32_t *tab,
                 const uint8_t *low, uint16_t *out, uint64_t n, uint32_t block, uint32_t K, int elem);
 
-/* nwc_dequant with the row index from nwc_row_index (layout 0, device; NULL: none) and the 13-bit decode table from
+/* nwc_dequant with the row index from nwc_row_index (layouts 0/1, device; NULL: none) and the 13-bit decode table from
  * nwc_seq_table (device; layouts 0/1; NULL: none), block fixed at 4096.  With the index, small matrices split each
- * block's rows over two or four half-waves; with the table, fewer decode steps take the slow path.  Same output.
+ * block over two or four half-waves; with the table, fewer decode steps take the slow path.  Same output.
  * No counterpart in the reference. */
 int nwc_dequant_seq(void *stream, const uint8_t *data, const uint32_t *bases, const uint8_t *hdr, const uint32_t *tab,
                     const uint8_t *low, const uint16_t *row_index, const uint32_t *seq_table, uint16_t *out, uint64_t n,

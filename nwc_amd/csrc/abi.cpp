@@ -146,7 +146,7 @@ bool plan_layout1_budget(const Shape &f, int mode, int ncu, bool index, uint32_t
     const uint32_t CB = f.CB, groups = f.groups();
     const uint32_t G = std::max(1u, (groups + 2u * (uint32_t)ncu - 1u) / (2u * (uint32_t)ncu)), blocks = G * CB;
     for (uint32_t sp : {4u, 2u, 1u}) {
-        if (sp > 1 ? !(index && rows) : (mode != kRowIndex && mode != kDequant)) continue;
+        if (sp > 1 ? !(index && (rows || mode == kDequant)) : (mode != kRowIndex && mode != kDequant)) continue;
         const uint32_t halves = (blocks * sp + 1u) & ~1u;
         if (halves > 32u) continue;
         const uint32_t part = rows ? G * kRows12 * CB * sp * 4u + (f.K16 + 31u) / 32u * 64u : 0u;   // + x as BF16
@@ -284,7 +284,7 @@ extern "C" int nwc_dequant_seq(void *stream, const uint8_t *data, const uint32_t
     if (!shape_ok(n, kBlock, K, elem)) return -1;
     const int layout = elem_layout(elem);
     return run_blocks(kDequant, true, (hipStream_t)stream, data, bases, hdr, tab, low, nullptr, nullptr, nullptr, out, n, K,
-                      elem, layout == 0 ? row_index : nullptr, layout <= 1 ? seq_table : nullptr);
+                      elem, layout <= 1 ? row_index : nullptr, layout <= 1 ? seq_table : nullptr);
 }
 
 extern "C" int nwc_linear_bf16(void *stream, const uint8_t *data, const uint32_t *bases, const uint8_t *hdr, const uint32_t *tab,

@@ -991,6 +991,12 @@ static int launch_layout1_token(const LaunchPlan &p, const BlockArgs &a, hipStre
 }
 
 // Layout 1, single round.
+template <int ELEM, int MODE, bool XBF16, int NS, int PEEK>
+static void launch_ns(bool full, dim3 g, dim3 b, uint32_t lds, hipStream_t st, const BlockArgs &a) {
+    if (full) hipLaunchKernelGGL((k_layout1s<ELEM, MODE, XBF16, NS, true, PEEK>), g, b, lds, st, a);
+    else hipLaunchKernelGGL((k_layout1s<ELEM, MODE, XBF16, NS, false, PEEK>), g, b, lds, st, a);
+}
+
 template <int ELEM, int MODE, bool XBF16>
 static int launch_layout1s(const LaunchPlan &p, const BlockArgs &a, hipStream_t st) {
     const bool full = Shape(a.M, a.K, 1).nsl == 16u;
@@ -1005,14 +1011,15 @@ static int launch_layout1s(const LaunchPlan &p, const BlockArgs &a, hipStream_t 
         else hipLaunchKernelGGL((k_layout1s<ELEM, MODE, XBF16, 16, false>), g, b, p.lds, st, a);
         return (int)hipGetLastError();
     }
-    if constexpr (MODE == kDequant) {                          // one half-wave per block
-        if (p.split != 1) return -1;
+    if constexpr (MODE == kDequant) {                          // one, two or four half-waves per block
         if (p.seq13) {
-            if (full) hipLaunchKernelGGL((k_layout1s<ELEM, MODE, XBF16, 16, true, kPeekSeq>), g, b, p.lds, st, a);
-            else hipLaunchKernelGGL((k_layout1s<ELEM, MODE, XBF16, 16, false, kPeekSeq>), g, b, p.lds, st, a);
+            if (p.split == 4) launch_ns<ELEM, MODE, XBF16, 4, kPeekSeq>(full, g, b, p.lds, st, a);
+            else if (p.split == 2) launch_ns<ELEM, MODE, XBF16, 8, kPeekSeq>(full, g, b, p.lds, st, a);
+            else launch_ns<ELEM, MODE, XBF16, 16, kPeekSeq>(full, g, b, p.lds, st, a);
         } else {
-            if (full) hipLaunchKernelGGL((k_layout1s<ELEM, MODE, XBF16, 16, true>), g, b, p.lds, st, a);
-            else hipLaunchKernelGGL((k_layout1s<ELEM, MODE, XBF16, 16, false>), g, b, p.lds, st, a);
+            if (p.split == 4) launch_ns<ELEM, MODE, XBF16, 4, kPeek>(full, g, b, p.lds, st, a);
+            else if (p.split == 2) launch_ns<ELEM, MODE, XBF16, 8, kPeek>(full, g, b, p.lds, st, a);
+            else launch_ns<ELEM, MODE, XBF16, 16, kPeek>(full, g, b, p.lds, st, a);
         }
         return (int)hipGetLastError();
     }

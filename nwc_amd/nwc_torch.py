@@ -355,7 +355,7 @@ class NWCWeight:
         w = out if out is not None else torch.empty((self.out_features, self.K16), dtype=torch.bfloat16, device=self.data.device)
         st = self.seq_table() if self.layout <= 1 else None
         if st is not None:
-            ri = self.row_index() if self.layout == 0 else None
+            ri = self.row_index() if self.layout <= 1 else None
             err = _lib.nwc_dequant_seq(_stream(), _ptr(self.data), _ptr(self.bases), _ptr(self.hdr), _ptr(self.lut),
                                        _ptr(self.low), _ptr(ri) if ri is not None else None, _ptr(st), _ptr(w), self.n,
                                        self.in_features, self.code)

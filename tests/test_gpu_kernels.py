@@ -331,7 +331,7 @@ def test_dequant_with_and_without_table(cuda, layout, M, K, escapes):
     for seq in (False, True):
         out = torch.full((M, c.K16), -1, dtype=torch.int16, device="cuda")
         if seq:
-            ri = c.row_index() if layout == 0 else None
+            ri = c.row_index() if layout <= 1 else None
             err = _lib.nwc_dequant_seq(_stream(), _ptr(c.data), _ptr(c.bases), _ptr(c.hdr), _ptr(c.lut), _ptr(c.low),
                                        _ptr(ri) if ri is not None else None, _ptr(st) if st is not None else None,
                                        _ptr(out), c.n, K, c.code)
