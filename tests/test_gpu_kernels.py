@@ -287,7 +287,7 @@ def test_token_path_with_and_without_row_index(cuda, layout, M, K, split, escape
 
 @pytest.mark.parametrize("M,K,escapes", [(4608, 3584, "none"), (3584, 3584, "dense"), (1003, 1100, "dense"),
                                           (16, 512, "none"), (2000, 3000, "dense"), (37888, 3584, "dense"),
-                                          (3584, 18944, "none")])
+                                          (3584, 18944, "none"), (1000, 17000, "dense")])
 def test_layout2_split_token_path(cuda, M, K, escapes):
     """Layout 2's token path on matrices with few 16-row groups per CU, where a block's 16 super-chunks go to four or
     two half-waves (qkv / o of Qwen2.5-7B, ragged shapes), and on gate_up / down of Qwen2.5-7B (tiles with more
