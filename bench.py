@@ -388,7 +388,6 @@ def greedy_token(lg, width=128):
     elements and an argmax over those: every reduction stays inside one workgroup.  A single argmax over a 151936-entry
     vocabulary is a multi-workgroup reduction whose zero-initialised counters a captured HIP graph does not reset
     correctly on later replays."""
-    import torch
     import torch.nn.functional as F
     n = lg.numel()
     rows = F.pad(lg, (0, (-n) % width), value=float("-inf")).view(-1, width)
