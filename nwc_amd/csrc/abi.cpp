@@ -122,10 +122,11 @@ bool plan_layout0_tiers(const Shape &f, int mode, int ncu, bool index, uint32_t 
     }
 }
 
-// Layout 1, single round, for the token path with the row index: G whole 16-row groups per workgroup (two workgroups
-// per CU), SP = 4 or 2 half-waves per block, at most 32 half-waves; a region buffer of up to 880 words per block (a
-// 16 x 512 block of N(0, 0.02^2) BF16 needs ~700, real model weights ~760).  Building the index itself uses SP = 1
-// (decoding from global memory: the region is larger than the copy's four chunks per thread).  False otherwise: the
+// Layout 1, single round, for the token path and dequantization with the row index: G whole 16-row groups per
+// workgroup (two workgroups per CU), SP = 4 or 2 half-waves per block, at most 32 half-waves; a region buffer of up to
+// 880 words per block (a 16 x 512 block of N(0, 0.02^2) BF16 needs ~700, real model weights ~760).  Building the index
+// itself uses SP = 1 (decoding from global memory: the region is larger than the copy's four chunks per thread), and
+// so does dequantization without the index (its copy finishes the region in a second pass).  False otherwise: the
 // caller then uses the multi-block kernel.
 constexpr uint32_t kSlotWords1s = 880, kSlotWords1Min = 768;
 constexpr uint32_t kDynLdsOne = 128u * 1024u;         // dynamic LDS of a workgroup that has its CU to itself
