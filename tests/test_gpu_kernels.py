@@ -396,3 +396,48 @@ def test_reference_gather_shapes(cuda, layout, M, K):
     out = out.cpu()
     assert torch.all(out[[0, 1, 3]] == 0x1234)
     assert torch.equal(out[2, :K], w[0].view(torch.int16))
+
+
+def _random_shapes(n, seed):
+    """Seeded log-uniform shapes (M up to 3000, K up to 20000): ragged K16/K32 tails, column-block counts from 1 to 40,
+    row counts that leave partial row groups."""
+    g = np.random.default_rng(seed)
+    return [(int(np.exp(g.uniform(0, np.log(3000)))), int(np.exp(g.uniform(0, np.log(20000)))),
+             int(g.integers(0, 3)), ["bf16", "fp8"][int(g.integers(0, 2))]) for _ in range(n)]
+
+
+@pytest.mark.parametrize("M,K,layout,elem", _random_shapes(24, 20261202))
+def test_random_shapes_all_paths(cuda, M, K, layout, elem):
+    """Seeded random shapes through every path: dequant (bit-exact against the source for BF16; both entry points
+    agree), gather, token path (BF16 x) within one BF16 ulp of float64 on the decoded weights (fp8: times the row
+    scale), fp32 path within 1e-3."""
+    from nwc_amd.nwc_torch import _lib, _ptr, _stream
+    NWCWeight, _, _ = _nwc()
+    print(f"random shape {M}x{K} layout {layout} {elem}", flush=True)
+    src = fp8_source(M, K, seed=M * 31 + K) if elem == "fp8" else bf16_matrix(M, K, seed=M * 31 + K)
+    try:
+        c = NWCWeight(src, device="cuda", layout=layout, elem=elem)
+    except (RuntimeError, ValueError):
+        # a matrix the format cannot code (a lane stream over 255 words, or over 255 layout-2 exceptions): the
+        # oracle's restatement of the reference encoder refuses it too
+        _, _, quantize_fp8 = _nwc()
+        codes = quantize_fp8(src)[0].view(torch.uint8).numpy() if elem == "fp8" else bits16(src)
+        assert O.encode(codes, int(elem == "fp8"), layout)["dl"] < 0
+        return
+    d = c.dequant()
+    w = d.float() * c.scale[:, None] if elem == "fp8" else d.float()
+    if elem == "bf16":
+        assert torch.equal(d.cpu().view(torch.int16), src.view(torch.int16))
+    out = torch.empty(M, c.K16, dtype=torch.bfloat16, device="cuda")
+    assert _lib.nwc_dequant(_stream(), _ptr(c.data), _ptr(c.bases), _ptr(c.hdr), _ptr(c.lut), _ptr(c.low), _ptr(out),
+                            c.n, c.block, K, c.code) == 0
+    assert torch.equal(out[:, :K], d)
+    ids = torch.randint(0, M, (9,), generator=torch.Generator().manual_seed(K))
+    rows = c.gather(ids.cuda())                                 # fp8: the unscaled values, as dequant()
+    assert torch.equal(rows.view(torch.int16), d[ids.cuda()].view(torch.int16))
+    x = torch.randn(K, generator=torch.Generator().manual_seed(M)).to(torch.bfloat16).cuda()
+    y = c.linear_bf16(x, None).double().cpu().numpy()
+    y64 = (w.double() @ x.double()).cpu().numpy()
+    assert np.all(np.abs(y - y64) <= 2.0 ** -8 * np.abs(y64) + 1e-5)
+    y32 = c.matvec(x.float()).double().cpu().numpy()
+    assert np.all(np.abs(y32 - y64) <= 1e-3 * np.abs(y64) + 1e-5)
