@@ -441,3 +441,30 @@ def test_random_shapes_all_paths(cuda, M, K, layout, elem):
     assert np.all(np.abs(y - y64) <= 2.0 ** -8 * np.abs(y64) + 1e-5)
     y32 = c.matvec(x.float()).double().cpu().numpy()
     assert np.all(np.abs(y32 - y64) <= 1e-3 * np.abs(y64) + 1e-5)
+
+
+@pytest.mark.parametrize("layout", LAYOUTS)
+def test_special_values_round_trip(cuda, layout):
+    """BF16 specials survive bit for bit: +-0, +-inf, NaNs with several payloads, subnormals, the largest finite
+    values, scattered through an N(0, 0.02^2) matrix (dequant, gather, and the oracle's decode of the same tensors)."""
+    NWCWeight, _, _ = _nwc()
+    M, K = 64, 1100
+    w = bf16_matrix(M, K, seed=99, escapes=False)
+    bits = w.view(torch.int16).view(-1)
+    specials = [0x0000, 0x8000, 0x7F80, 0xFF80, 0x7FC0, 0xFFC1, 0x7F81, 0x0001, 0x8001, 0x007F, 0x7F7F, 0xFF7F, 0x3F80]
+    g = torch.Generator().manual_seed(3)
+    pos = torch.randint(0, M * K, (400,), generator=g)
+    for i, p in enumerate(pos.tolist()):
+        v = specials[i % len(specials)]
+        bits[p] = v - 0x10000 if v >= 0x8000 else v
+    if layout == 2:
+        try:
+            c = NWCWeight(w, device="cuda", layout=layout)
+        except ValueError:
+            pytest.skip("a lane stream has more than 255 layout-2 exceptions")
+    else:
+        c = NWCWeight(w, device="cuda", layout=layout)
+    assert torch.equal(c.dequant().cpu().view(torch.int16), w.view(torch.int16))
+    assert np.array_equal(O.decode(oracle_encoding(c)), bits16(w))
+    ids = torch.unique(pos // K)[:16]
+    assert torch.equal(c.gather(ids.cuda()).cpu().view(torch.int16), w[ids].view(torch.int16))
