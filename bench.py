@@ -22,6 +22,9 @@ The other BASELINE configs, each printed as one JSON line of its own (not the dr
   --prefill 512            configs[2] prefill: per matrix, dequantization to a BF16 buffer + hipBLASLt GEMM of 512
                            tokens, against the GEMM on resident BF16 weights
   --gather 64              configs[4] embedding: 64 seeded ids from the 152064x3584 table, layouts 0, 1 and 2
+  --decode 128             model level: greedy decode of a random-init Qwen3 (--config qwen3-4b or qwen3-0.6b), one
+                           HIP graph per token, BF16 (hipBLASLt) against NWC (--decode-elem bf16 or fp8)
+  --encode                 the host encoder on configs[0] against the single-threaded oracle restatement (no GPU)
 usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--layout 0] [--cpu-seconds 10] [--config NAME]
        python bench.py --profile-launches 20     (counter target for rocprofv3 --pmc: copies + gate_up launches;
                                                  --profile-shape qkv|o|gate_up|down picks the matrix)
