@@ -571,3 +571,13 @@ uint8_t or_f32_to_e4m3(float v) {
     }
     return (uint8_t)(sg | best);
 }
+
+void or_quantize_e4m3(const float *v, uint64_t n, uint8_t *out, int threads) {
+#ifdef _OPENMP
+    if (threads > 0) omp_set_num_threads(threads);
+#else
+    (void)threads;
+#endif
+    #pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < (int64_t)n; i++) out[i] = or_f32_to_e4m3(v[i]);
+}

@@ -51,6 +51,8 @@ int or_linear(const uint8_t *data, uint64_t data_len, const uint32_t *bases, con
 uint8_t or_f32_to_e4m3(float v);
 /* fp8 e4m3fn byte -> fp32, from the definition (e >= 1: 2^(e-7) (1 + m/8); e = 0: m 2^-9). */
 float or_e4m3_to_f32(uint8_t b);
+/* or_f32_to_e4m3 over an array (OpenMP; threads <= 0: all). */
+void or_quantize_e4m3(const float *v, uint64_t n, uint8_t *out, int threads);
 
 /* The fp8 split tables (nwc_ops.cu:140-148, :165-173) exposed for the exhaustive known-answer tests. */
 int or_fp8_split(uint8_t b, uint8_t *sym, uint8_t *nib);

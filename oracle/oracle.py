@@ -49,6 +49,7 @@ def lib():
         L.or_linear.restype = I; L.or_linear.argtypes = [P, U64, P, P, P, P, U64, U32, I, P, P, P, I]
         L.or_f32_to_e4m3.restype = ctypes.c_uint8; L.or_f32_to_e4m3.argtypes = [ctypes.c_float]
         L.or_e4m3_to_f32.restype = ctypes.c_float; L.or_e4m3_to_f32.argtypes = [ctypes.c_uint8]
+        L.or_quantize_e4m3.restype = None; L.or_quantize_e4m3.argtypes = [P, U64, P, I]
         for fn in ("or_fp8_split", "or_fp8_split2"):
             getattr(L, fn).restype = I
             getattr(L, fn).argtypes = [ctypes.c_uint8, P, P]
@@ -140,21 +141,15 @@ def bf16_to_f64(bits):
     return (bits.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
 
 
-def f32_to_bf16_rne(v):
-    """Round-to-nearest-even fp32 -> BF16 bits (the finalize rounding of nwc_ops.cu:562-564), from the definition."""
-    u = np.ascontiguousarray(v, np.float32).view(np.uint32).astype(np.uint64)
-    r = (u + 0x7FFF + ((u >> 16) & 1)) >> 16
-    return r.astype(np.uint16)
-
-
 def quantize_fp8(w_f32):
-    """nwc_torch.py:88-94 restated: per-row scale = max(absmax, 1e-12) / 448, q = RNE_e4m3(clamp(w / scale))."""
-    w = np.asarray(w_f32, np.float32)
+    """nwc_torch.py:88-94 restated: per-row scale = max(absmax, 1e-12) / 448 in fp32, then each weight
+    q = RNE_e4m3(clamp(w / scale, -448, 448)) through or_f32_to_e4m3 (nearest of the 127 finite codes, ties to
+    the even code).  Returns (uint8 codes [M, K], float32 scale [M])."""
+    w = np.ascontiguousarray(w_f32, np.float32)
     scale = (np.maximum(np.abs(w).max(axis=1), np.float32(1e-12)) / np.float32(448.0)).astype(np.float32)
-    v = np.clip(w / scale[:, None], -448.0, 448.0).astype(np.float32)
-    f = lib().or_f32_to_e4m3
-    table_in = v.ravel()
-    q = np.fromiter((f(float(t)) for t in table_in), dtype=np.uint8, count=table_in.size).reshape(w.shape)
+    v = np.ascontiguousarray(np.clip(w / scale[:, None], np.float32(-448.0), np.float32(448.0)), np.float32)
+    q = np.zeros(v.shape, np.uint8)
+    lib().or_quantize_e4m3(_p(v), v.size, _p(q), 0)
     return q, scale
 
 
