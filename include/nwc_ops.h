@@ -8,8 +8,9 @@
  * buffer belong to the caller.  `elem` = element type (0 BF16, 1 fp8 e4m3fn) | layout << 4 (layouts 0, 1, 2).
  * `block` must be 4096 (nwc_info(4)); K is the number of columns, n = M * K.
  *
- * Device entry points return 0, -1 for a shape the format cannot describe (or, in this build, a layout-0 raw plane
- * of 4 GB or more: M * K16 >= 2^32), or a hipError_t code of the launch.  `low` must be followed by the format's 512
+ * Device entry points return 0, -1 for a shape the format cannot describe (or, in this build, a raw plane the
+ * kernels cannot address with 32-bit offsets: layout 0 with Mp * K16 >= 2^32 for Mp = M rounded up to 8 rows,
+ * layouts 1/2 with a plane of 2^32 - 512 bytes or more), or a hipError_t code of the launch.  `low` must be followed by the format's 512
  * slack bytes (nwc_torch.py:43); the kernels read into them.
  */
 #ifndef NWC_OPS_H

@@ -23,13 +23,19 @@ int current_cus() {
     return c;
 }
 
-// nwc_ops.cu:1050: the fixed block of 4096 weights, M = n / K within 32 bits, and a known element type / layout
-// This build also addresses the layout-0 raw plane with 32-bit offsets: M * K16 < 2^32 (4 GB planes).
+// nwc_ops.cu:1050: the fixed block of 4096 weights, M = n / K within 32 bits, and a known element type / layout.
+// This build also addresses the raw planes with 32-bit offsets: layout 0 counts weights of the padded matrix
+// (Mp * K16, rows past M included), layouts 1/2 count bytes of the plane padded to 16 rows and 32 columns plus its
+// 512 slack bytes; both must stay below 2^32.
 bool shape_ok(uint64_t n, uint32_t block, uint32_t K, int elem) {
     if (!(block == kBlock && K != 0 && n % K == 0 && n / K >= 1 && n / K <= 0xFFFFFFFFull && elem_type(elem) <= 1 &&
           elem_layout(elem) <= 2 && (elem & ~0xFF) == 0))
         return false;
-    return (n / K) * (uint64_t)((K + 15u) & ~15u) < (1ull << 32);
+    const uint64_t M = n / K, K16 = (K + 15u) & ~15u;
+    if (M * K16 >= (1ull << 32)) return false;          // also keeps Shape's 32-bit fields (M < 2^28) from wrapping
+    const Shape f((uint32_t)M, K, elem_layout(elem));
+    if (elem_layout(elem) == 0) return (uint64_t)f.Mp * f.K16 < (1ull << 32);
+    return f.low_bytes(elem) + kRawSlack < (1ull << 32);
 }
 
 // LDS words per half-wave for a staged block: an 8 x 512 block of N(0, 0.02^2) BF16 needs ~370 words, real model

@@ -81,3 +81,43 @@ def test_layout_rejects():
     assert lib.nwc_layout(0, 16, 0, out.ctypes.data) == -1
     assert lib.nwc_layout(16, 0, 0, out.ctypes.data) == -1
     assert lib.nwc_layout(1 << 32, 16, 0, out.ctypes.data) == -1
+
+
+def _device_entry(lib):
+    P, U64, U32, I = ctypes.c_void_p, ctypes.c_uint64, ctypes.c_uint32, ctypes.c_int
+    lib.nwc_linear_bf16.restype = I
+    lib.nwc_linear_bf16.argtypes = [P, P, P, P, P, P, P, P, P, P, P, U64, U32, U32, I]
+    lib.nwc_matvec.restype = I
+    lib.nwc_matvec.argtypes = [P, P, P, P, P, P, P, P, U64, U32, U32, I]
+    lib.nwc_linear_xbf16.restype = I
+    lib.nwc_linear_xbf16.argtypes = [P, P, P, P, P, P, P, P, P, P, P, P, U64, U32, I]
+    return lib
+
+
+@pytest.mark.parametrize("M,K,elem,ok", [
+    ((1 << 20) - 1, 4096, 0x10, False),   # layout 1: M * K16 = 2^32 - 4096, but the plane padded to 16 rows is 2^32 B
+    ((1 << 20) - 1, 4096, 0x20, False),   # layout 2: nibble + raw planes beyond 2^32 bytes
+    ((1 << 20) - 1, 4096, 0x00, False),   # layout 0: rows padded to 8 reach 2^32 weights
+    ((1 << 28), 16, 0x00, False),         # M * K16 = 2^32
+    ((1 << 20) - 1, 4096, 0x11, True),    # layout 1 fp8: 8 bytes per lane and super-chunk, 2^31 bytes
+    ((1 << 20) - 8, 4096, 0x00, True),    # layout 0 just below the bound
+])
+def test_device_entry_points_refuse_unaddressable_planes(M, K, elem, ok):
+    """Shapes whose raw plane the kernels cannot address with 32-bit offsets get -1 from every device entry point
+    before any device call (null pointers; no GPU needed).  Accepted shapes are probed only through nwc_token_split,
+    which launches nothing."""
+    from oracle import oracle as O
+    lib = _device_entry(_lib())
+    lib.nwc_token_split.restype = ctypes.c_int
+    lib.nwc_token_split.argtypes = [ctypes.c_uint64, ctypes.c_uint32, ctypes.c_int, ctypes.c_int]
+    n = M * K
+    _, n_low, _, K16 = O.layout_info(M, K, elem & 15, elem >> 4)
+    if elem >> 4:
+        assert (n_low + 512 < (1 << 32)) == ok
+    if ok:
+        assert lib.nwc_token_split(n, K, elem, 0) != -1
+        return
+    assert lib.nwc_token_split(n, K, elem, 0) == -1
+    assert lib.nwc_linear_bf16(None, *([None] * 10), n, 4096, K, elem) == -1
+    assert lib.nwc_matvec(None, *([None] * 7), n, 4096, K, elem) == -1
+    assert lib.nwc_linear_xbf16(None, *([None] * 11), n, K, elem) == -1
