@@ -81,7 +81,7 @@ class Launch:
     """One prepared nwc_linear_xbf16 call (ctypes arguments built once)."""
 
     def __init__(self, c, x, y):
-        from nwc_amd.nwc_torch import _lib, _ptr
+        from nwc_amd._abi import lib as _lib, ptr as _ptr
         self.fn = _lib.nwc_linear_xbf16
         ri, st = c.row_index(), c.seq_table()
         self.args = [_ptr(c.data), _ptr(c.bases), _ptr(c.hdr), _ptr(c.lut), _ptr(c.low),
@@ -460,15 +460,16 @@ def compressed_weights_equal(model, orig):
     NWCEmbedding and fused-projection slice of a converted model against the BF16 state dict taken before conversion
     (fp8 matrices: against quantize_fp8 of it)."""
     import torch
-    from nwc_amd.nwc_torch import NWCEmbedding, NWCLinear, _FusedHead
+    from nwc_amd.nwc_torch import NWCEmbedding, NWCLinear, _FusedSlice
     checked = bad = 0
     last = (None, None)
     for name, m in model.named_modules():
-        if isinstance(m, _FusedHead):
-            lin = m.g["lin"]
+        if isinstance(m, _FusedSlice):
+            lin = m.group.lin
             if last[0] is not lin:
                 last = (lin, lin.w.dequant()[:, :lin.in_features])
-            w = last[1][m.start:m.end]
+            start = m.group.starts[m.index]
+            w = last[1][start:start + m.group.sizes[m.index]]
         elif isinstance(m, (NWCLinear, NWCEmbedding)):
             w = m.w.dequant()[:, :m.w.in_features]
         else:
@@ -486,7 +487,7 @@ def compressed_weights_equal(model, orig):
 
 
 def m_elem(m):
-    w = m.g["lin"].w if hasattr(m, "g") else m.w
+    w = m.group.lin.w if hasattr(m, "group") else m.w
     return "fp8" if w.scale is not None else "bf16"
 
 
@@ -631,13 +632,14 @@ def run_encode(args):
     is single-threaded too), outputs byte-identical.  No GPU needed."""
     import numpy as np
     import torch
-    from nwc_amd.nwc_torch import _lib, _ptr, NPAIR, HDR_BLOCK, RAW_SLACK, _layout_info
+    from nwc_amd._abi import lib as _lib, ptr as _ptr
+    from nwc_amd.nwc_torch import NPAIR, HDR_BLOCK, RAW_SLACK, _geometry
     from oracle import oracle as O
     M, K = 9728, 2560
     w = make_weight(M, K, 7)
     src = w.view(torch.int16).contiguous()
     n = M * K
-    nb, n_low, _, _ = _layout_info(M, K, 0)
+    nb, n_low, _, _ = _geometry(M, K, 0)
     cap = n + n // 2 + nb * 64 + 4096
     bufs = dict(freq=torch.empty(NPAIR, dtype=torch.int16), psym=torch.empty(NPAIR, dtype=torch.int16),
                 bases=torch.empty(nb, dtype=torch.int32), hdr=torch.empty(nb * HDR_BLOCK, dtype=torch.uint8),

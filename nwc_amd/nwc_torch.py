@@ -1,76 +1,45 @@
-"""NWC for PyTorch on AMD Instinct MI355X: NWCLinear keeps BF16 (or weight-only fp8) weights losslessly compressed in
-HBM.
+"""PyTorch side of NWC on AMD Instinct MI355X: modules that keep BF16 (or weight-only fp8) weights losslessly
+compressed in HBM and multiply through the gfx950 library.
 
-    batch 1 (token generation) -> fused decode-matvec kernel (decoded in registers, nwc_linear_xbf16)
-    otherwise (prefill)        -> decompression into a temporary BF16 buffer + F.linear (hipBLASLt)
+    one token (batch 1)  -> fused decode-matvec kernel, weights decoded in registers (nwc_linear_xbf16)
+    several tokens       -> the matrix decompressed into a temporary BF16 buffer, then F.linear (hipBLASLt)
 
-Mirror of the reference bridge parda21/NWC nwc/nwc_torch.py: same classes, functions, arguments, buffer contracts and
-errors, over the gfx950 C-ABI library nwc_amd/lib/nwc_ops.so (include/nwc_ops.h).  There is no CPU fallback: the
-compute entry points need the HIP library and a GPU, the host encoder needs only the library.
+The public names, arguments, buffer contracts and exceptions are those of the reference bridge (parda21/NWC
+nwc/nwc_torch.py: NWCWeight :126-269, NWCLinear :306-327, NWCEmbedding :330-344, fuse :360-386, convert :389-445,
+quantize_fp8 :88-94, RefFP8Linear :272-290), so code written against `nwc` runs against `nwc_amd`.  The structure
+below is this package's own.  There is no CPU fallback: compute methods need the HIP library and a GPU; the host
+encoder needs only the library.
 """
-import ctypes
 import os
+from typing import NamedTuple
 
 import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-LANES = 32
-NPAIR = 1024                      # size of the freq/psym buffers of the ABI
-RAW_SLACK = 512                   # bytes appended to the raw plane (nwc_torch.py:43)
+from . import _abi
+from ._abi import call, lib, ptr, stream
 
-
-def _find_library():
-    """Search order as in the reference (nwc_torch.py:14-22): NWC_DLL, then the package's lib/ directory."""
-    here = os.path.dirname(os.path.abspath(__file__))
-    candidates = [os.environ.get("NWC_DLL"), os.path.join(here, "lib", "nwc_ops.so")]
-    for c in candidates:
-        if c and os.path.exists(c):
-            return c
-    raise ImportError("NWC library not found: run `python -m nwc_amd.build` (needs hipcc, builds for gfx950); looked for "
-                      + ", ".join(c for c in candidates if c))
-
-
-_LIB_PATH = _find_library()
-_lib = ctypes.CDLL(_LIB_PATH)
-P = ctypes.c_void_p
-U64, U32, I32 = ctypes.c_uint64, ctypes.c_uint32, ctypes.c_int
-_lib.nwc_info.restype = I32; _lib.nwc_info.argtypes = [I32]
-VERSION, NSTATE, TAB_WORDS, HDR_BLOCK = (_lib.nwc_info(i) for i in range(4))
-FIXED_BLOCK = _lib.nwc_info(4)
-ELEM = _lib.nwc_info(5) == 1
-LAYOUT1 = _lib.nwc_info(6) == 1
-LAYOUT2 = _lib.nwc_info(7) == 1
+_LIB_PATH = _abi.LIB_PATH
+VERSION, NSTATE, TAB_WORDS, HDR_BLOCK, FIXED_BLOCK = (_abi.VERSION, _abi.NSTATE, _abi.TAB_WORDS, _abi.HDR_BLOCK,
+                                                      _abi.FIXED_BLOCK)
+ELEM, LAYOUT1, LAYOUT2 = _abi.HAS_ELEM, _abi.HAS_LAYOUT1, _abi.HAS_LAYOUT2
 V9 = VERSION >= 9
 X_FP32 = True                     # the reference ABI's layout-0 token path takes x as fp32
+
+LANES = 32                        # lane streams per block
+NPAIR = 1024                      # length of the encoder's freq/psym buffers
+RAW_SLACK = 512                   # bytes after the raw plane `low` that the kernels may read
+DATA_SLACK = 64                   # zero bytes kept after the encoder's output in `data`
+SEQ_TABLE_WORDS = 8196            # 13-bit decode table + exp_of_rank
 ELEM_BF16, ELEM_FP8 = 0, 1
 ELEMS = {"bf16": ELEM_BF16, "fp8": ELEM_FP8}
-LAYOUTS = {0, 1, 2}
-LAYOUT_DEFAULT = {ELEM_BF16: 0, ELEM_FP8: 0}
-if "NWC_LAYOUT" in os.environ:
-    LAYOUT_DEFAULT = {k: int(os.environ["NWC_LAYOUT"]) for k in LAYOUT_DEFAULT}
-
-_lib.nwc_layout.restype = I32; _lib.nwc_layout.argtypes = [U64, U32, I32, P]
-_lib.nwc_encode.restype = ctypes.c_int64; _lib.nwc_encode.argtypes = [P, U64, U32, I32, P, P, P, P, P, U64, P]
-_lib.nwc_build_tab.restype = None; _lib.nwc_build_tab.argtypes = [P, P, I32, P]
-_lib.nwc_matvec.restype = I32; _lib.nwc_matvec.argtypes = [P, P, P, P, P, P, P, P, U64, U32, U32, I32]
-_lib.nwc_dequant.restype = I32; _lib.nwc_dequant.argtypes = [P, P, P, P, P, P, P, U64, U32, U32, I32]
-_lib.nwc_linear_bf16.restype = I32
-_lib.nwc_linear_bf16.argtypes = [P, P, P, P, P, P, P, P, P, P, P, U64, U32, U32, I32]
-_lib.nwc_linear_xbf16.restype = I32
-_lib.nwc_linear_xbf16.argtypes = [P, P, P, P, P, P, P, P, P, P, P, P, U64, U32, I32]
-_lib.nwc_dequant_seq.restype = I32
-_lib.nwc_dequant_seq.argtypes = [P, P, P, P, P, P, P, P, P, U64, U32, I32]
-_lib.nwc_seq_table.restype = I32
-_lib.nwc_seq_table.argtypes = [P, I32, P]
-_lib.nwc_row_index.restype = I32; _lib.nwc_row_index.argtypes = [P, P, P, P, P, P, P, U64, U32, I32]
-_lib.nwc_token_split.restype = I32; _lib.nwc_token_split.argtypes = [U64, U32, I32, I32]
-SEQ_TABLE = os.environ.get("NWC_SEQ_TABLE", "1") != "0"     # layout 0: the 13-bit token-path decode table
-SEQ_TABLE_WORDS = 8196
+LAYOUTS = (0, 1, 2)
+_default_layout = int(os.environ.get("NWC_LAYOUT", "0"))
+LAYOUT_DEFAULT = {ELEM_BF16: _default_layout, ELEM_FP8: _default_layout}
+SEQ_TABLE = os.environ.get("NWC_SEQ_TABLE", "1") != "0"   # layouts 0/1: stage the 13-bit decode table
 ROW_INDEX = os.environ.get("NWC_ROW_INDEX", "1") != "0"   # layouts 0/1: build the row index for the token path
-_lib.nwc_gather.restype = I32; _lib.nwc_gather.argtypes = [P, P, P, P, P, P, P, U32, P, U64, U32, U32, I32]
-_lib.nwc_ref_fp8.restype = I32; _lib.nwc_ref_fp8.argtypes = [P, P, P, P, P, U64, U32]
-_lib.nwc_setup.restype = I32; _lib.nwc_setup.argtypes = []
+FP8_MAX = 448.0
 
 
 def _check_layout(layout):
@@ -78,316 +47,574 @@ def _check_layout(layout):
         raise ValueError(f"unknown layout {layout}")
 
 
-def _ptr(t):
-    return ctypes.c_void_p(t.data_ptr())
-
-
-def _stream():
-    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
-
-
 def _need_gpu(t):
     if t.device.type != "cuda":
         raise RuntimeError("NWC kernels run on the GPU: move the NWCWeight to a cuda device")
 
 
-FP8_MAX = 448.0
+# ---------------------------------------------------------------------------------------------------------------
+# weight-only fp8
+
+def _absmax_scale(wf):
+    """Per-row fp32 scale: absmax / 448, with absmax floored at 1e-12 so all-zero rows divide safely."""
+    return wf.abs().amax(dim=1).clamp_min(1e-12) / FP8_MAX
 
 
 def quantize_fp8(w: torch.Tensor):
-    """BF16/float [out, in] -> (fp8 e4m3fn tensor, fp32 scale[out]): symmetric absmax scale per output channel
-    (nwc_torch.py:88-94)."""
+    """[out, in] BF16 or float -> (float8_e4m3fn codes, fp32 scale[out]).  Each row is divided by its scale,
+    clamped to +-448 and rounded to nearest even e4m3 (reference nwc_torch.py:88-94)."""
     wf = w.detach().float()
-    scale = wf.abs().amax(dim=1).clamp_min(1e-12) / FP8_MAX
-    q = (wf / scale[:, None]).clamp(-FP8_MAX, FP8_MAX).to(torch.float8_e4m3fn)
-    return q, scale
+    scale = _absmax_scale(wf)
+    scaled = torch.clamp(wf / scale.unsqueeze(1), min=-FP8_MAX, max=FP8_MAX)
+    return scaled.to(torch.float8_e4m3fn), scale
 
 
 def ref_fp8_matvec(w8: torch.Tensor, scale: torch.Tensor, x_f32: torch.Tensor) -> torch.Tensor:
-    """Uncompressed fp8 weight-only matvec in the library (the bandwidth baseline): y = scale * (W8 x), y BF16."""
+    """Uncompressed fp8 weight-only matvec of the library (the bandwidth baseline): BF16 y = scale * (W8 x)."""
     _need_gpu(w8)
-    M, K = w8.shape
-    y = torch.empty(M, dtype=torch.bfloat16, device=w8.device)
-    xin = (x_f32 if x_f32.numel() % 16 == 0 else F.pad(x_f32, (0, 16 - x_f32.numel() % 16))).contiguous()
-    err = _lib.nwc_ref_fp8(_stream(), _ptr(w8.view(torch.uint8)), _ptr(scale), _ptr(xin), _ptr(y), M, K)
-    if err:
-        raise RuntimeError(f"nwc_ref_fp8 HIP error {err}")
+    rows, cols = w8.shape
+    y = torch.empty(rows, dtype=torch.bfloat16, device=w8.device)
+    pad = -x_f32.numel() % 16
+    xin = (F.pad(x_f32, (0, pad)) if pad else x_f32).contiguous()
+    call("nwc_ref_fp8", stream(), ptr(w8.view(torch.uint8)), ptr(scale), ptr(xin), ptr(y), rows, cols)
     return y
 
 
 def fits(out_features, in_features):
-    """Whether a matrix of this shape can be compressed (format v9+ pads any shape to its blocks)."""
-    return in_features >= 1 and out_features >= 1
+    """Whether the format can hold a matrix of this shape: any size, padded to whole blocks."""
+    return out_features >= 1 and in_features >= 1
 
 
 def choose_block(n):
-    """The format's fixed block of 4096 weights."""
+    """Weights per block: fixed at 4096 (8 x 512) by the format."""
     return FIXED_BLOCK
 
 
-def _layout_info(out_f, in_f, code):
-    lay = torch.empty(4, dtype=torch.int64)
-    if _lib.nwc_layout(out_f, in_f, code, _ptr(lay)):
-        raise RuntimeError("nwc_layout")
-    return lay.tolist()
+# ---------------------------------------------------------------------------------------------------------------
+# host-side encoding and validation of the compressed tensors
+
+class _Geometry(NamedTuple):
+    blocks: int           # 8 x 512 (layout 0) or 16 x 512 (layouts 1/2) blocks
+    raw_bytes: int        # bytes of the raw plane `low`, without its slack
+    scratch_floats: int   # Mp * CB, the reference's partial-sum scratch
+    K16: int              # in_features rounded up to 16
 
 
-def _check_streams(bases, hdr, data_len, layout, elem):
-    """Structural check of stored tensors before the kernels read them: every block's lane streams (or exception
-    lists) end inside `data` with the decoder's read-ahead slack."""
+def _geometry(rows, cols, code) -> _Geometry:
+    out = torch.empty(4, dtype=torch.int64)
+    if lib.nwc_layout(rows, cols, code, ptr(out)):
+        raise RuntimeError(f"nwc_layout refused a {rows} x {cols} matrix")
+    return _Geometry(*out.tolist())
+
+
+def _encoder_capacities(n, blocks):
+    """data buffers to try: about 4 bits per weight first (streams of real or Gaussian weights need under 3), then
+    the worst case of 24 bits per weight (every weight an escape or an exception)."""
+    slack = 64 * blocks + 4096
+    return (n // 2 + slack, 3 * n + slack)
+
+
+def _encode(src, rows, cols, code):
+    """Run the host encoder on row-major source bits (int16 BF16 or uint8 fp8, CPU).  Returns the five stored
+    tensors on the CPU: data (the encoder's bytes + DATA_SLACK zero bytes), bases, hdr, lut, low (+ RAW_SLACK)."""
+    geo = _geometry(rows, cols, code)
+    n = rows * cols
+    freq = torch.empty(NPAIR, dtype=torch.int16)
+    psym = torch.empty(NPAIR, dtype=torch.int16)
+    bases = torch.empty(geo.blocks, dtype=torch.int32)
+    hdr = torch.empty(geo.blocks * HDR_BLOCK, dtype=torch.uint8)
+    low = torch.zeros(geo.raw_bytes + RAW_SLACK, dtype=torch.uint8)
+    length, buf = -1, None
+    for cap in _encoder_capacities(n, geo.blocks):
+        buf = torch.empty(cap, dtype=torch.uint8)
+        length = lib.nwc_encode(ptr(src), n, cols, code, ptr(freq), ptr(psym), ptr(bases), ptr(hdr), ptr(buf), cap,
+                                ptr(low))
+        if length != -1:
+            break
+    if length == -2:
+        raise ValueError("fp8 weights contain NaN")
+    if length == -3:
+        raise ValueError("layout 2 cannot code this matrix (a lane stream has more than 255 exceptions); "
+                         "use layout 0 or 1")
+    if length < 0:
+        raise RuntimeError(f"nwc_encode failed ({length})")
+    lut = torch.empty(TAB_WORDS, dtype=torch.int32)
+    lib.nwc_build_tab(ptr(freq), ptr(psym), code, ptr(lut))
+    data = torch.zeros(length + DATA_SLACK, dtype=torch.uint8)
+    data[:length] = buf[:length]
+    return {"data": data, "bases": bases, "hdr": hdr, "lut": lut, "low": low}, length, geo
+
+
+def _validate_streams(bases, hdr, data_len, layout, elem):
+    """Structural check of stored tensors before any kernel reads them.  Block bases are 8-byte aligned byte
+    offsets; every block's lane streams (layouts 0/1: 4 bytes per header word) or exception entries (layout 2: 3
+    bytes, fp8 2) end at or before the next block's base, and the last block's end leaves the decoder's read-ahead
+    slack inside `data`.  A tensor set that breaks this (a corrupt or foreign checkpoint) would make the kernels
+    read outside their buffers, so it is refused with ValueError."""
     if bases.numel() == 0:
         return
-    h = hdr.to(torch.int64).view(-1, LANES).sum(1)
-    esz = 4 if layout != 2 else (2 if elem == ELEM_FP8 else 3)
-    end = bases.to(torch.int64) + h * esz + (64 if layout != 2 else 0)
-    if int(bases.to(torch.int64).min()) < 0 or int(end.max()) > data_len:
+    start = bases.to(torch.int64) & 0xFFFFFFFF
+    words = hdr.to(torch.int64).view(-1, LANES).sum(1)
+    unit = 4 if layout != 2 else (2 if elem == ELEM_FP8 else 3)
+    end = start + words * unit
+    tail = DATA_SLACK if layout != 2 else 0
+    if bool((start % 8 != 0).any()):
+        raise ValueError("block bases are not 8-byte aligned: corrupt checkpoint")
+    if bool((start[1:] < end[:-1]).any()):
+        raise ValueError("block streams overlap or go backwards: corrupt checkpoint")
+    if int(end[-1]) + tail > data_len:
         raise ValueError("compressed streams run past the data tensor: corrupt checkpoint")
 
 
+# ---------------------------------------------------------------------------------------------------------------
+
 class NWCWeight:
-    """Compressed representation of an [out, in] matrix on the GPU.
-    elem "bf16": the BF16 weights, lossless.  elem "fp8": weight-only fp8 e4m3 with a per-output-channel fp32 scale
-    (from a BF16 matrix via quantize_fp8, or a float8 tensor plus `scale`), the fp8 values stored lossless."""
+    """An [out, in] matrix held compressed on the GPU.
+    elem "bf16": the BF16 weights, lossless.  elem "fp8": weight-only fp8 e4m3 with an fp32 scale per output row
+    (quantized here from a BF16 matrix, or given as a float8 tensor plus `scale`); the fp8 codes are stored lossless.
+    The stored tensors are the format's (data, bases, hdr, lut, low, and scale for fp8); the row index and the
+    13-bit decode table are derived from them on first use and are not part of the format."""
 
     def __init__(self, w: torch.Tensor, device="cuda", block=None, elem="bf16", scale=None, layout=None):
-        assert w.dim() == 2
-        out_f, in_f = w.shape
-        assert fits(out_f, in_f), f"shape {tuple(w.shape)} not supported"
-        self.elem = ELEMS[elem]
-        self.layout = LAYOUT_DEFAULT[self.elem] if layout is None else int(layout)
-        _check_layout(self.layout)
-        if self.elem == ELEM_FP8:
-            if w.dtype == torch.float8_e4m3fn:
-                if scale is None:
-                    raise ValueError("fp8 weights need their per-row scale")
-                q = w
-            else:
-                q, scale = quantize_fp8(w)
-            src = q.detach().contiguous().cpu().view(torch.uint8)
-            self.scale = scale.detach().float().contiguous().to(device)
-        else:
+        assert w.dim() == 2, "a 2-D weight matrix is expected"
+        rows, cols = w.shape
+        assert fits(rows, cols), f"shape {tuple(w.shape)} not supported"
+        kind = ELEMS[elem]
+        layout = LAYOUT_DEFAULT[kind] if layout is None else int(layout)
+        _check_layout(layout)
+        src, scale = self._source(w, kind, scale)
+        self._shape(rows, cols, block, kind, layout)
+        stored, length, geo = _encode(src, rows, cols, self.code)
+        self._place(stored, scale, device, geo)
+        self.bytes = self._stored_bytes(length)
+
+    @staticmethod
+    def _source(w, kind, scale):
+        """Row-major source bits on the CPU and the fp32 row scale (fp8 only)."""
+        if kind == ELEM_BF16:
             assert w.dtype == torch.bfloat16, "BF16 expected (elem='fp8' for fp8 weights)"
-            src = w.detach().contiguous().cpu().view(torch.int16)
-            self.scale = None
-        n = out_f * in_f
-        block = block or choose_block(n)
-        nb, n_low, n_scratch, self.K16 = _layout_info(out_f, in_f, self.code)
-        freq = torch.empty(NPAIR, dtype=torch.int16)
-        psym = torch.empty(NPAIR, dtype=torch.int16)
-        bases = torch.empty(nb, dtype=torch.int32)
-        hdr = torch.empty(nb * HDR_BLOCK, dtype=torch.uint8)
-        low = torch.zeros(n_low + RAW_SLACK, dtype=torch.uint8)
-        dl = -1
-        for cap in (n + n // 2 + nb * 64 + 4096, 3 * n + nb * 64 + 4096):   # same capacity ladder as nwc_torch.py:163
-            data = torch.empty(cap, dtype=torch.uint8)
-            dl = _lib.nwc_encode(_ptr(src), n, in_f, self.code, _ptr(freq), _ptr(psym), _ptr(bases), _ptr(hdr),
-                                 _ptr(data), cap, _ptr(low))
-            if dl >= 0 or dl in (-2, -3):
-                break
-        if dl == -2:
-            raise ValueError("fp8 weights contain NaN")
-        if dl == -3:
-            raise ValueError("layout 2 cannot code this matrix (a lane stream has more than 255 exceptions); use layout 0 or 1")
-        if dl < 0:
-            raise RuntimeError("nwc_encode failed")
-        lut = torch.empty(TAB_WORDS, dtype=torch.int32)
-        _lib.nwc_build_tab(_ptr(freq), _ptr(psym), self.code, _ptr(lut))
-        self.out_features, self.in_features, self.n, self.block = out_f, in_f, n, block
-        stored = torch.zeros(dl + 64, dtype=torch.uint8)            # the encoder writes data[0 .. dl); the rest is slack
-        stored[:dl] = data[:dl]
-        self.data = stored.to(device)
-        self.bases = bases.to(device)
-        self.hdr = hdr.to(device)
-        self.lut = lut.to(device)
-        self.low = low.to(device)
-        self._finish(dl, n_low, n_scratch)
+            return w.detach().contiguous().cpu().view(torch.int16), None
+        if w.dtype == torch.float8_e4m3fn:
+            if scale is None:
+                raise ValueError("fp8 weights need their per-row scale")
+            codes = w
+        else:
+            codes, scale = quantize_fp8(w)
+        return codes.detach().contiguous().cpu().view(torch.uint8), scale.detach().float().contiguous()
+
+    def _shape(self, rows, cols, block, kind, layout):
+        self.out_features, self.in_features = rows, cols
+        self.n = rows * cols
+        self.block = block or choose_block(self.n)
+        self.elem, self.layout = kind, layout
+
+    def _place(self, stored, scale, device, geo):
+        for name in ("data", "bases", "hdr", "lut", "low"):
+            setattr(self, name, stored[name].to(device))
+        self.scale = None if scale is None else scale.float().to(device)
+        self.K16 = geo.K16
+        self._raw_bytes, self._n_scratch = geo.raw_bytes, geo.scratch_floats
+        self._scratch = self._row_index = self._seq_table = None
+        self.bytes_bf16 = 2 * self.n
+        self.bytes_native = self.n + 4 * self.out_features if self.elem == ELEM_FP8 else 2 * self.n
+
+    def _stored_bytes(self, stream_bytes):
+        """Compressed size: streams + bases + header + table + raw plane (+ fp8 scale), the reference's `bytes`."""
+        scale = 4 * self.scale.numel() if self.scale is not None else 0
+        return stream_bytes + 4 * self.bases.numel() + self.hdr.numel() + 4 * self.lut.numel() + self._raw_bytes + scale
+
+    @classmethod
+    def from_tensors(cls, out_f, in_f, block, data, bases, hdr, lut, low, device="cuda", elem="bf16", scale=None,
+                     layout=0):
+        """Rebuild from stored tensors (a checkpoint), without the original weights.  Tensors that do not match the
+        shape, or whose streams are malformed, raise ValueError before anything reaches the GPU."""
+        self = cls.__new__(cls)
+        kind, layout = ELEMS[elem], int(layout)
+        _check_layout(layout)
+        self._shape(out_f, in_f, block, kind, layout)
+        geo = _geometry(out_f, in_f, self.code)
+        if (bases.numel() != geo.blocks or hdr.numel() != geo.blocks * HDR_BLOCK or lut.numel() != TAB_WORDS
+                or low.numel() not in (geo.raw_bytes, geo.raw_bytes + RAW_SLACK)):
+            raise ValueError("checkpoint does not match this library version")
+        _validate_streams(bases.cpu(), hdr.cpu(), data.numel(), layout, kind)
+        if low.numel() == geo.raw_bytes:
+            low = F.pad(low, (0, RAW_SLACK))
+        self._place({"data": data, "bases": bases, "hdr": hdr, "lut": lut, "low": low}, scale, device, geo)
+        self.bytes = self._stored_bytes(self.data.numel())
+        return self
+
+    def tensors(self):
+        """The stored tensors (what a checkpoint keeps)."""
+        out = {name: getattr(self, name) for name in ("data", "bases", "hdr", "lut", "low")}
+        if self.scale is not None:
+            out["scale"] = self.scale
+        return out
 
     @property
     def code(self):
-        """elem parameter of the library: element type in bits 0..3, layout in bits 4..7."""
+        """The library's `elem` argument: element type in bits 0-3, layout in bits 4-7."""
         return self.elem | (self.layout << 4)
-
-    def _finish(self, dl, n_low, n_scratch):
-        n = self.n
-        self.bytes = (dl + self.bases.numel() * 4 + self.hdr.numel() + self.lut.numel() * 4 + n_low
-                      + (self.scale.numel() * 4 if self.scale is not None else 0))
-        self.bytes_bf16 = 2 * n
-        self.bytes_native = n + self.out_features * 4 if self.elem == ELEM_FP8 else 2 * n
-        self._n_scratch = n_scratch
-        self._scratch = None
 
     @property
     def scratch(self):
-        """fp32 [Mp * CB] scratch of the reference ABI; the gfx950 kernels reduce inside the workgroup and do not use
-        it, so it is only allocated when asked for."""
+        """fp32 [Mp * CB] scratch of the reference ABI.  The gfx950 kernels reduce the column-block partial sums
+        inside a workgroup and never touch it, so it is allocated only when asked for."""
         if self._scratch is None:
             self._scratch = torch.empty(self._n_scratch, dtype=torch.float32, device=self.data.device)
         return self._scratch
 
-    @classmethod
-    def from_tensors(cls, out_f, in_f, block, data, bases, hdr, lut, low, device="cuda", elem="bf16", scale=None, layout=0):
-        """Compressed representation from stored tensors (nwc_amd.checkpoint), without the originals."""
-        self = cls.__new__(cls)
-        self.elem = ELEMS[elem]
-        self.layout = int(layout)
-        _check_layout(self.layout)
-        n = out_f * in_f
-        nb, n_low, n_scratch, self.K16 = _layout_info(out_f, in_f, self.code)
-        if bases.numel() != nb or low.numel() not in (n_low, n_low + RAW_SLACK) or hdr.numel() != nb * HDR_BLOCK \
-                or lut.numel() != TAB_WORDS:
-            raise ValueError("checkpoint does not match this library version")
-        _check_streams(bases.cpu(), hdr.cpu(), data.numel(), self.layout, self.elem)
-        self.out_features, self.in_features, self.n, self.block = out_f, in_f, n, block
-        if low.numel() == n_low:
-            low = F.pad(low, (0, RAW_SLACK))
-        self.data, self.bases, self.hdr, self.lut, self.low = (t.to(device) for t in (data, bases, hdr, lut, low))
-        self.scale = None if scale is None else scale.float().to(device)
-        self._finish(self.data.numel() - 64, n_low, n_scratch)
-        self.bytes = (self.data.numel() + self.bases.numel() * 4 + self.hdr.numel() + self.lut.numel() * 4 + n_low
-                      + (self.scale.numel() * 4 if self.scale is not None else 0))
-        return self
+    def _streams(self):
+        return ptr(self.data), ptr(self.bases), ptr(self.hdr), ptr(self.lut), ptr(self.low)
 
-    def tensors(self):
-        """The tensors that fully describe the compressed state (for nwc_amd.checkpoint)."""
-        t = {"data": self.data, "bases": self.bases, "hdr": self.hdr, "lut": self.lut, "low": self.low}
-        if self.scale is not None:
-            t["scale"] = self.scale
-        return t
-
-    def _x16(self, x):
-        """Extend x to K16 (layout 0) or K rounded up to 32 (layouts 1/2) with zeros."""
-        kp = (self.in_features + 31) // 32 * 32 if self.layout else self.K16
-        return x if kp == self.in_features else F.pad(x, (0, kp - self.in_features))
-
-    def matvec(self, x_f32: torch.Tensor) -> torch.Tensor:
-        """fp32 test path: y = W x with fp32 output (times scale for fp8)."""
-        _need_gpu(self.data)
-        y = torch.empty(self.out_features, dtype=torch.float32, device=x_f32.device)
-        xin = self._x16(x_f32.contiguous().float())
-        err = _lib.nwc_matvec(_stream(), _ptr(self.data), _ptr(self.bases), _ptr(self.hdr), _ptr(self.lut),
-                              _ptr(self.low), _ptr(xin), _ptr(y), self.n, self.block, self.in_features, self.code)
-        if err:
-            raise RuntimeError(f"nwc_matvec HIP error {err}")
-        return y if self.scale is None else y * self.scale
-
+    # ---- derived structures (built once per matrix) ----
     def row_index(self):
-        """Row index (uint16 [blocks x 3 x 32], built on the GPU on first use; not part of the format): each lane's bit
-        position at rows 2, 4, 6 (layout 0) or super-chunks 4, 8, 12 (layout 1), so the token kernel can split a block
-        over two or four half-waves.  None for layout 2, for layout-1 shapes whose index kernel has no single-round
-        plan (K > 16384), or with NWC_ROW_INDEX=0."""
+        """uint16 [blocks x 3 x 32]: each lane's bit position at rows 2, 4, 6 (layout 0) or super-chunks 4, 8, 12
+        (layout 1), built on the GPU on first use, so the token kernels can split a block over two or four
+        half-waves.  None for layout 2, for layout-1 shapes the index kernel has no plan for, or with
+        NWC_ROW_INDEX=0."""
         if self.layout > 1 or not ROW_INDEX:
             return None
-        ri = getattr(self, "_row_index", None)
-        if ri is None:
+        if self._row_index is None:
             _need_gpu(self.data)
-            ri = torch.empty(self.bases.numel() * 3 * LANES, dtype=torch.int16, device=self.data.device)
-            err = _lib.nwc_row_index(_stream(), _ptr(self.data), _ptr(self.bases), _ptr(self.hdr), _ptr(self.lut),
-                                     _ptr(self.low), _ptr(ri), self.n, self.in_features, self.code)
-            if err == -1 and self.layout == 1:
-                ri = False                                         # no plan for this shape: decode without an index
-            elif err:
-                raise RuntimeError(f"nwc_row_index error {err}")
-            self._row_index = ri
-        return ri if ri is not False else None
+            index = torch.empty(self.bases.numel() * 3 * LANES, dtype=torch.int16, device=self.data.device)
+            rc = lib.nwc_row_index(stream(), *self._streams(), ptr(index), self.n, self.in_features, self.code)
+            if rc == -1 and self.layout == 1:
+                index = False                                  # no plan for this shape: decode without an index
+            elif rc:
+                raise RuntimeError(f"nwc_row_index error {rc}")
+            self._row_index = index
+        return self._row_index if self._row_index is not False else None
 
     def seq_table(self):
-        """The 13-bit token-path decode table of layouts 0/1 (int32 [8196] on the device, built on the host from the
-        stored LUT on first use; not part of the format), or None for layout 2 or with NWC_SEQ_TABLE=0."""
+        """int32 [8196] 13-bit decode table of layouts 0/1 on the device, built on the host from the stored LUT on
+        first use.  None for layout 2 or with NWC_SEQ_TABLE=0."""
         if self.layout > 1 or not SEQ_TABLE:
             return None
-        st = getattr(self, "_seq_table", None)
-        if st is None:
-            host = torch.empty(SEQ_TABLE_WORDS, dtype=torch.int32)
-            lut = self.lut.cpu().contiguous()                      # held: the library reads it through a raw pointer
-            if _lib.nwc_seq_table(_ptr(lut), self.code, _ptr(host)):
+        if self._seq_table is None:
+            table = torch.empty(SEQ_TABLE_WORDS, dtype=torch.int32)
+            lut = self.lut.cpu().contiguous()
+            if lib.nwc_seq_table(ptr(lut), self.code, ptr(table)):
                 raise RuntimeError("nwc_seq_table failed")
-            st = self._seq_table = host.to(self.data.device)
-        return st
+            self._seq_table = table.to(self.data.device)
+        return self._seq_table
 
     def token_bytes(self):
-        """Algorithmic bytes one token-path call reads: the compressed matrix, plus the row-index entries the kernel
-        uses (64 bytes per block when it splits blocks over two half-waves, 192 over four) and the 13-bit table."""
-        split = _lib.nwc_token_split(self.n, self.in_features, self.code, int(self.row_index() is not None))
+        """Bytes one token-path call reads: the compressed matrix, the row-index entries its plan uses (64 per block
+        at two half-waves per block, 192 at four) and the 13-bit table."""
+        split = lib.nwc_token_split(self.n, self.in_features, self.code, int(self.row_index() is not None))
         table = 4 * SEQ_TABLE_WORDS if self.seq_table() is not None else 0
         return self.bytes + self.bases.numel() * LANES * 2 * (split - 1) + table
 
+    # ---- compute ----
+    def _padded(self, x):
+        """x zero-extended to the kernels' width: K16 (layout 0) or in_features rounded up to 32 (layouts 1/2)."""
+        width = -(-self.in_features // 32) * 32 if self.layout else self.K16
+        extra = width - self.in_features
+        return (F.pad(x, (0, extra)) if extra else x).contiguous()
+
+    def matvec(self, x_f32: torch.Tensor) -> torch.Tensor:
+        """fp32 test path: y = W x in fp32 (times the row scale for fp8)."""
+        _need_gpu(self.data)
+        y = torch.empty(self.out_features, dtype=torch.float32, device=x_f32.device)
+        xin = self._padded(x_f32.float())
+        call("nwc_matvec", stream(), *self._streams(), ptr(xin), ptr(y), self.n, self.block, self.in_features,
+             self.code)
+        return y if self.scale is None else y * self.scale
+
     def linear_bf16(self, x: torch.Tensor, bias) -> torch.Tensor:
-        """Token path: y = scale * (W x) + bias, x BF16 or fp32, y BF16."""
+        """Token path: BF16 y = scale * (W x) + bias for one activation vector (BF16 or fp32)."""
         _need_gpu(self.data)
         y = torch.empty(self.out_features, dtype=torch.bfloat16, device=x.device)
-        bp = _ptr(bias) if bias is not None else None
-        sp = _ptr(self.scale) if self.scale is not None else None
         if x.dtype == torch.bfloat16 or self.layout:
-            xin = self._x16(x if x.dtype == torch.bfloat16 else x.to(torch.bfloat16)).contiguous()
-            ri, st = self.row_index(), self.seq_table()
-            err = _lib.nwc_linear_xbf16(_stream(), _ptr(self.data), _ptr(self.bases), _ptr(self.hdr), _ptr(self.lut),
-                                        _ptr(self.low), _ptr(ri) if ri is not None else None,
-                                        _ptr(st) if st is not None else None, _ptr(xin), bp, sp, _ptr(y),
-                                        self.n, self.in_features, self.code)
-        else:                                                      # layout 0 with fp32 activations: the reference ABI
-            xin = self._x16(x.float()).contiguous()
-            err = _lib.nwc_linear_bf16(_stream(), _ptr(self.data), _ptr(self.bases), _ptr(self.hdr), _ptr(self.lut),
-                                       _ptr(self.low), _ptr(xin), bp, sp, None, _ptr(y), self.n, self.block,
-                                       self.in_features, self.code)
-        if err:
-            raise RuntimeError(f"nwc_linear_bf16 HIP error {err}")
+            # BF16 activations (layouts 1/2 always take them): the extended entry point with the derived structures
+            xin = self._padded(x.to(torch.bfloat16))
+            call("nwc_linear_xbf16", stream(), *self._streams(), ptr(self.row_index()), ptr(self.seq_table()),
+                 ptr(xin), ptr(bias), ptr(self.scale), ptr(y), self.n, self.in_features, self.code)
+        else:
+            # layout 0 with fp32 activations: the reference's entry point
+            xin = self._padded(x.float())
+            call("nwc_linear_bf16", stream(), *self._streams(), ptr(xin), ptr(bias), ptr(self.scale), None, ptr(y),
+                 self.n, self.block, self.in_features, self.code)
         return y
 
     def gather(self, ids: torch.Tensor) -> torch.Tensor:
-        """Rows ids -> BF16[..., in_features] (embedding lookup straight from the compressed state)."""
+        """Rows `ids` as BF16 [..., in_features], decoded straight from the compressed matrix (embedding lookup)."""
         _need_gpu(self.data)
         flat = ids.reshape(-1).to(device=self.data.device, dtype=torch.int64).contiguous()
-        out = torch.empty(flat.numel(), self.K16, dtype=torch.bfloat16, device=self.data.device)
-        err = _lib.nwc_gather(_stream(), _ptr(self.data), _ptr(self.bases), _ptr(self.hdr), _ptr(self.lut),
-                              _ptr(self.low), _ptr(flat), flat.numel(), _ptr(out), self.n, self.block, self.in_features,
-                              self.code)
-        if err:
-            raise RuntimeError(f"nwc_gather HIP error {err}")
+        rows = torch.empty(flat.numel(), self.K16, dtype=torch.bfloat16, device=self.data.device)
+        call("nwc_gather", stream(), *self._streams(), ptr(flat), flat.numel(), ptr(rows), self.n, self.block,
+             self.in_features, self.code)
         if self.K16 != self.in_features:
-            out = out[:, :self.in_features].contiguous()
-        return out.view(*ids.shape, self.in_features)
+            rows = rows[:, :self.in_features].contiguous()
+        return rows.view(*ids.shape, self.in_features)
 
     def dequant(self, out: torch.Tensor = None) -> torch.Tensor:
-        """The full matrix as BF16 (row-major); a view with row stride K16 if K is not a multiple of 16.
-        fp8: the unscaled fp8 values (exact in BF16); multiply rows by `scale` for the weights.
-        `out` may supply a preallocated BF16 [out_features, K16] buffer (prefill keeps one per shape)."""
+        """The matrix decompressed to BF16, row-major; a view with row stride K16 when K is not a multiple of 16.
+        fp8: the unscaled fp8 values (exact in BF16).  `out` may supply a BF16 [out_features, K16] buffer."""
         _need_gpu(self.data)
-        w = out if out is not None else torch.empty((self.out_features, self.K16), dtype=torch.bfloat16, device=self.data.device)
-        st = self.seq_table() if self.layout <= 1 else None
-        if st is not None:
-            ri = self.row_index() if self.layout <= 1 else None
-            err = _lib.nwc_dequant_seq(_stream(), _ptr(self.data), _ptr(self.bases), _ptr(self.hdr), _ptr(self.lut),
-                                       _ptr(self.low), _ptr(ri) if ri is not None else None, _ptr(st), _ptr(w), self.n,
-                                       self.in_features, self.code)
+        if out is None:
+            out = torch.empty((self.out_features, self.K16), dtype=torch.bfloat16, device=self.data.device)
+        table = self.seq_table()
+        if table is not None:
+            call("nwc_dequant_seq", stream(), *self._streams(), ptr(self.row_index()), ptr(table), ptr(out), self.n,
+                 self.in_features, self.code)
         else:
-            err = _lib.nwc_dequant(_stream(), _ptr(self.data), _ptr(self.bases), _ptr(self.hdr), _ptr(self.lut),
-                                   _ptr(self.low), _ptr(w), self.n, self.block, self.in_features, self.code)
-        if err:
-            raise RuntimeError(f"nwc_dequant HIP error {err}")
-        return w if self.K16 == self.in_features else w[:, :self.in_features]
+            call("nwc_dequant", stream(), *self._streams(), ptr(out), self.n, self.block, self.in_features, self.code)
+        return out if self.K16 == self.in_features else out[:, :self.in_features]
 
     def dequant_fp8(self):
-        """fp8 weights: (float8_e4m3fn tensor [out, in], fp32 scale[out]), bit-exact with what was encoded."""
+        """fp8 matrices: (float8_e4m3fn [out, in], fp32 scale[out]), bit-exact with what was encoded."""
         if self.elem != ELEM_FP8:
             raise ValueError("not an fp8 matrix")
         return self.dequant().to(torch.float8_e4m3fn), self.scale
 
 
+# ---------------------------------------------------------------------------------------------------------------
+# modules
+
+def _bf16_bias(bias, device):
+    if bias is None:
+        return None
+    return nn.Parameter(bias.detach().to(device=device, dtype=torch.bfloat16), requires_grad=False)
+
+
+class NWCLinear(nn.Module):
+    """nn.Linear over a compressed matrix (elem "bf16" lossless, or "fp8" weight-only).  One BF16 token goes through
+    the fused decode-matvec kernel; anything else through a temporary BF16 matrix and F.linear."""
+
+    def __init__(self, linear: nn.Linear = None, device="cuda", block=None, w: "NWCWeight" = None, bias=None,
+                 elem="bf16"):
+        super().__init__()
+        self.w = NWCWeight(linear.weight.data, device, block, elem=elem) if w is None else w
+        self.in_features, self.out_features = self.w.in_features, self.w.out_features
+        if linear is not None and linear.bias is not None:
+            bias = linear.bias.data
+        self.bias = _bf16_bias(bias, device)
+
+    def _bias_data(self):
+        return None if self.bias is None else self.bias.data
+
+    def forward(self, x):
+        if x.dtype == torch.bfloat16 and x.numel() == self.in_features:
+            y = self.w.linear_bf16(x.contiguous().view(-1), self._bias_data())
+            return y.view(*x.shape[:-1], self.out_features)
+        weight = self.w.dequant()
+        if self.w.scale is None:
+            return F.linear(x, weight, self.bias)
+        # fp8: the product of the unscaled codes, then the row scale and the bias in fp32
+        y = F.linear(x, weight).float() * self.w.scale
+        if self.bias is not None:
+            y = y + self.bias.float()
+        return y.to(x.dtype)
+
+    def extra_repr(self):
+        kind = "fp8" if self.w.elem == ELEM_FP8 else "bf16"
+        return (f"in={self.in_features}, out={self.out_features}, elem={kind}, layout={self.w.layout}, "
+                f"{self.w.bytes / 1e6:.1f} MB compressed of {self.w.bytes_bf16 / 1e6:.1f} MB BF16")
+
+
+class NWCEmbedding(nn.Module):
+    """nn.Embedding over a compressed matrix (shared with a tied output projection); rows are decoded by the
+    gather kernel, fp8 rows then scaled."""
+
+    def __init__(self, emb: nn.Embedding = None, w: NWCWeight = None, padding_idx=None):
+        super().__init__()
+        self.w = w
+        self.num_embeddings, self.embedding_dim = w.out_features, w.in_features
+        self.padding_idx = padding_idx if emb is None else emb.padding_idx
+
+    def forward(self, ids):
+        rows = self.w.gather(ids)
+        if self.w.scale is None:
+            return rows
+        row_scale = self.w.scale[ids.to(self.w.scale.device)].unsqueeze(-1)
+        return (rows.float() * row_scale).to(torch.bfloat16)
+
+    def extra_repr(self):
+        return (f"{self.num_embeddings}, {self.embedding_dim}, {self.w.bytes / 1e6:.1f} MB compressed of "
+                f"{self.w.bytes_bf16 / 1e6:.1f} MB BF16")
+
+
+class _FusedGroup:
+    """Sibling projections that read the same input, concatenated into one compressed matrix.  The first slice
+    computes the whole product; later slices called with the same input tensor reuse it."""
+
+    def __init__(self, lin: NWCLinear, names, sizes):
+        self.lin, self.names, self.sizes = lin, list(names), list(sizes)
+        self.starts = [sum(self.sizes[:i]) for i in range(len(self.sizes))]
+        self._input = self._output = None
+
+    def output(self, index, x):
+        if index == 0 or self._input is not x or self._output is None:
+            self._output = self.lin(x)
+            self._input = x
+        a = self.starts[index]
+        return self._output[..., a:a + self.sizes[index]]
+
+
+class _FusedSlice(nn.Module):
+    """Stands in for one projection of a fused group: its rows of the group's output."""
+
+    def __init__(self, group: _FusedGroup, index):
+        super().__init__()
+        self.group, self.index = group, index
+        self.in_features, self.out_features = group.lin.in_features, group.sizes[index]
+
+    def forward(self, x):
+        return self.group.output(self.index, x)
+
+    def extra_repr(self):
+        return f"slice {self.index} of fused {'+'.join(self.group.names)}, out={self.out_features}"
+
+
+def _children(model, kind):
+    """(parent, attribute name, child) for every direct child of type `kind` anywhere in the model."""
+    for parent in list(model.modules()):
+        for name, child in list(parent.named_children()):
+            if isinstance(child, kind):
+                yield parent, name, child
+
+
+def _release(*params):
+    """Drop the host copies of converted weights."""
+    for p in params:
+        p.data = torch.empty(0)
+
+
+def _concat_bias(linears, dtype):
+    """Biases of fused projections: None if none has one, otherwise concatenated with zeros for the missing."""
+    if all(l.bias is None for l in linears):
+        return None
+    parts = [l.bias.data if l.bias is not None else torch.zeros(l.out_features, dtype=dtype) for l in linears]
+    return torch.cat(parts, 0)
+
+
+def fuse(model: nn.Module, groups=(("q_proj", "k_proj", "v_proj"), ("gate_proj", "up_proj")), device="cuda",
+         elem="bf16"):
+    """Concatenate sibling nn.Linear layers with the same input into one compressed matrix each (fewer, larger
+    kernel launches).  Call before `convert`.  Returns the number of fused groups."""
+    count = 0
+    for parent in list(model.modules()):
+        for names in groups:
+            linears = [getattr(parent, nm, None) for nm in names]
+            if not all(isinstance(l, nn.Linear) and l.weight.dtype == torch.bfloat16 for l in linears):
+                continue
+            if len({l.in_features for l in linears}) != 1:
+                continue
+            weight = torch.cat([l.weight.data for l in linears], 0)
+            if not fits(*weight.shape):
+                continue
+            lin = NWCLinear(w=NWCWeight(weight, device, elem=elem), bias=_concat_bias(linears, weight.dtype),
+                            device=device)
+            group = _FusedGroup(lin, names, [l.out_features for l in linears])
+            for index, (nm, l) in enumerate(zip(names, linears)):
+                setattr(parent, nm, _FusedSlice(group, index))
+                _release(l.weight)
+            count += 1
+    print(f"nwc_amd.fuse: {count} projection groups now share one compressed matrix each")
+    return count
+
+
+class _Tally:
+    def __init__(self):
+        self.nwc = self.bf16 = self.modules = 0
+        self.skipped = []
+
+    def add(self, w):
+        self.nwc += w.bytes
+        self.bf16 += w.bytes_bf16
+        self.modules += 1
+
+
+def _same_storage(a, b):
+    return a is b or (a.numel() > 0 and a.data_ptr() == b.data_ptr())
+
+
+def convert(model: nn.Module, device="cuda", verbose=True, tied=True, elem="bf16", embeddings=True):
+    """Replace the model's BF16 nn.Linear layers by NWCLinear (and embeddings by NWCEmbedding), then move the
+    model to `device`.  elem "bf16" is lossless; "fp8" stores weight-only fp8 e4m3 codes (per-row scale) losslessly.
+    tied: an output projection that shares its weight with an embedding becomes one compressed matrix serving
+    both (gather for the lookup, matvec for the logits).  embeddings: compress the other embedding tables too
+    (always lossless BF16).  Returns (bytes_nwc, bytes_bf16) of the compressed matrices."""
+    tally = _Tally()
+    tables = [e for _, _, e in _children(model, nn.Embedding)]
+    tied_tables, tied_linears = set(), set()
+
+    # 1. output projections tied to an embedding table
+    for parent, name, lin in list(_children(model, nn.Linear)):
+        table = next((e for e in tables if _same_storage(e.weight, lin.weight)), None)
+        if table is None:
+            continue
+        tied_tables.add(id(table))
+        tied_linears.add(id(lin))
+        if not (tied and table.weight.dtype == torch.bfloat16 and fits(*table.weight.shape)):
+            tally.skipped.append(f"{name} {tuple(lin.weight.shape)} [tied]")
+            continue
+        w = NWCWeight(table.weight.data, device, elem=elem)
+        setattr(parent, name, NWCLinear(lin, device, w=w))
+        for p2, n2, e2 in list(_children(model, nn.Embedding)):
+            if e2 is table:
+                setattr(p2, n2, NWCEmbedding(table, w))
+        tally.add(w)
+        _release(table.weight, lin.weight)
+
+    # 2. the other embedding tables (a table still tied to a BF16 projection stays as it is)
+    if embeddings:
+        for parent, name, table in list(_children(model, nn.Embedding)):
+            if id(table) in tied_tables or table.weight.dtype != torch.bfloat16 or table.weight.numel() == 0 \
+                    or not fits(*table.weight.shape):
+                continue
+            w = NWCWeight(table.weight.data, device, elem="bf16")
+            setattr(parent, name, NWCEmbedding(table, w))
+            tally.add(w)
+            _release(table.weight)
+
+    # 3. groups fused earlier
+    seen = set()
+    for module in model.modules():
+        if isinstance(module, _FusedSlice) and id(module.group) not in seen:
+            seen.add(id(module.group))
+            tally.add(module.group.lin.w)
+
+    # 4. every other BF16 linear layer
+    for parent, name, lin in list(_children(model, nn.Linear)):
+        if id(lin) in tied_linears:
+            continue                                           # tied to a table that stays BF16 (listed above)
+        if lin.weight.dtype == torch.bfloat16 and lin.weight.numel() and fits(lin.out_features, lin.in_features):
+            new = NWCLinear(lin, device, elem=elem)
+            setattr(parent, name, new)
+            tally.add(new.w)
+            _release(lin.weight)
+        else:
+            tally.skipped.append(f"{name} {tuple(lin.weight.shape)} [{lin.weight.dtype}]")
+
+    model.to(device)
+    if verbose:
+        ratio = tally.nwc / max(tally.bf16, 1)
+        print(f"nwc_amd.convert ({elem}): {tally.modules} matrices compressed, {tally.bf16 / 1e9:.2f} GB of BF16 held "
+              f"in {tally.nwc / 1e9:.2f} GB ({ratio:.4f})")
+        if tally.skipped:
+            print("  left as they were:", ", ".join(tally.skipped[:6]) + (" ..." if len(tally.skipped) > 6 else ""))
+    return tally.nwc, tally.bf16
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# the uncompressed fp8 baseline
+
 class RefFP8Linear(nn.Module):
-    """Comparison only: weight-only fp8 without compression, served by the library's uncompressed fp8 matvec at batch 1
-    and by dequantization + hipBLASLt otherwise (nwc_torch.py:272-290)."""
+    """Comparison only: weight-only fp8 without compression (same quantization as NWCWeight(elem="fp8")).  One
+    BF16 token goes through the library's uncompressed fp8 matvec; anything else through a BF16 copy and
+    F.linear."""
 
     def __init__(self, linear: nn.Linear, device="cuda"):
         super().__init__()
-        q, scale = quantize_fp8(linear.weight.data)
-        self.w8 = q.contiguous().to(device)
-        self.scale = scale.to(device)
+        codes, scale = quantize_fp8(linear.weight.data)
+        self.w8, self.scale = codes.contiguous().to(device), scale.to(device)
         self.in_features, self.out_features = linear.in_features, linear.out_features
-        self.bias = None if linear.bias is None else nn.Parameter(
-            linear.bias.data.to(device=device, dtype=torch.bfloat16), requires_grad=False)
+        self.bias = _bf16_bias(None if linear.bias is None else linear.bias.data, device)
 
     def forward(self, x):
-        if x.numel() == self.in_features and x.dtype == torch.bfloat16:
+        if x.dtype == torch.bfloat16 and x.numel() == self.in_features:
             y = ref_fp8_matvec(self.w8, self.scale, x.reshape(-1).float())
             if self.bias is not None:
                 y = y + self.bias
@@ -399,181 +626,17 @@ class RefFP8Linear(nn.Module):
 
 
 def convert_ref_fp8(model: nn.Module, device="cuda", verbose=True):
-    """Replace every nn.Linear by RefFP8Linear (the uncompressed fp8 baseline); a tied lm_head stays BF16."""
-    shared = {m.weight.data_ptr() for m in model.modules() if isinstance(m, nn.Embedding)}
-    n = 0
-    for name, mod in list(model.named_modules()):
-        for child, cm in list(mod.named_children()):
-            if isinstance(cm, nn.Linear) and cm.weight.dtype == torch.bfloat16 and cm.weight.data_ptr() not in shared:
-                setattr(mod, child, RefFP8Linear(cm, device))
-                cm.weight.data = torch.empty(0)
-                n += 1
+    """Replace every BF16 nn.Linear by RefFP8Linear; a projection tied to an embedding stays BF16.  Returns the
+    number of replaced layers."""
+    tables = [e.weight for _, _, e in _children(model, nn.Embedding)]
+    count = 0
+    for parent, name, lin in list(_children(model, nn.Linear)):
+        if lin.weight.dtype != torch.bfloat16 or any(_same_storage(t, lin.weight) for t in tables):
+            continue
+        setattr(parent, name, RefFP8Linear(lin, device))
+        _release(lin.weight)
+        count += 1
     model.to(device)
     if verbose:
-        print(f"reference fp8: {n} linear layers replaced (uncompressed fp8, reference matvec)")
-    return n
-
-
-class NWCLinear(nn.Module):
-    """Drop-in replacement for nn.Linear on a compressed matrix (elem "bf16" lossless, or "fp8" weight-only)."""
-
-    def __init__(self, linear: nn.Linear = None, device="cuda", block=None, w: "NWCWeight" = None, bias=None, elem="bf16"):
-        super().__init__()
-        self.w = w if w is not None else NWCWeight(linear.weight.data, device, block, elem=elem)
-        self.in_features, self.out_features = self.w.in_features, self.w.out_features
-        if linear is not None and linear.bias is not None:
-            bias = linear.bias.data
-        self.bias = None if bias is None else nn.Parameter(bias.to(device=device, dtype=torch.bfloat16), requires_grad=False)
-
-    def forward(self, x):
-        if x.numel() == self.in_features and x.dtype == torch.bfloat16:   # one token -> fused kernel
-            xf = x if x.is_contiguous() else x.contiguous()
-            y = self.w.linear_bf16(xf.view(-1), None if self.bias is None else self.bias.data)
-            return y.view(*x.shape[:-1], self.out_features)
-        if self.w.scale is None:
-            return F.linear(x, self.w.dequant(), self.bias)          # prefill -> temporary decompression + hipBLASLt
-        y = F.linear(x, self.w.dequant()).float() * self.w.scale      # fp8: unscaled product, then the row scale
-        if self.bias is not None:
-            y = y + self.bias.float()
-        return y.to(x.dtype)
-
-    def extra_repr(self):
-        return (f"in={self.in_features}, out={self.out_features}, elem={'fp8' if self.w.elem else 'bf16'}, layout={self.w.layout}, "
-                f"{self.w.bytes/1e6:.1f} MB (BF16: {self.w.bytes_bf16/1e6:.1f} MB)")
-
-
-class NWCEmbedding(nn.Module):
-    """nn.Embedding replacement on a compressed matrix (shares the weight with a tied lm_head)."""
-
-    def __init__(self, emb: nn.Embedding = None, w: NWCWeight = None, padding_idx=None):
-        super().__init__()
-        self.w = w
-        self.num_embeddings, self.embedding_dim = w.out_features, w.in_features
-        self.padding_idx = emb.padding_idx if emb is not None else padding_idx
-
-    def forward(self, ids):
-        rows = self.w.gather(ids)
-        if self.w.scale is None:
-            return rows
-        return (rows.float() * self.w.scale[ids.to(self.w.scale.device)][..., None]).to(torch.bfloat16)
-
-    def extra_repr(self):
-        return f"{self.num_embeddings}, {self.embedding_dim}, {self.w.bytes/1e6:.1f} MB (BF16: {self.w.bytes_bf16/1e6:.1f} MB)"
-
-
-class _FusedHead(nn.Module):
-    """One output slice of a fused projection: head 0 computes the whole fused matvec, the others pick up their slice
-    (nwc_torch.py:347-357)."""
-
-    def __init__(self, shared, index, start, end):
-        super().__init__()
-        self.g, self.index, self.start, self.end = shared, index, start, end
-        self.in_features, self.out_features = shared["lin"].in_features, end - start
-
-    def forward(self, x):
-        g = self.g
-        if self.index == 0 or g["x_id"] != id(x) or g["y"] is None:
-            g["y"] = g["lin"](x)
-            g["x_id"] = id(x)
-        return g["y"][..., self.start:self.end]
-
-
-def fuse(model: nn.Module, groups=(("q_proj", "k_proj", "v_proj"), ("gate_proj", "up_proj")), device="cuda", elem="bf16"):
-    """Concatenate sibling nn.Linear layers with the same input into one NWC matrix (fewer, larger kernel launches).
-    Call before `convert`; the fused layers are NWC afterwards.  Returns the number of fused groups."""
-    n_fused = 0
-    for mod in list(model.modules()):
-        for names in groups:
-            lins = [getattr(mod, nm, None) for nm in names]
-            if not all(isinstance(l, nn.Linear) for l in lins):
-                continue
-            if len({l.in_features for l in lins}) != 1 or any(l.weight.dtype != torch.bfloat16 for l in lins):
-                continue
-            W = torch.cat([l.weight.data for l in lins], 0)
-            if not fits(W.shape[0], W.shape[1]):
-                continue
-            b = None
-            if all(l.bias is not None for l in lins):
-                b = torch.cat([l.bias.data for l in lins], 0)
-            elif any(l.bias is not None for l in lins):
-                b = torch.cat([l.bias.data if l.bias is not None else torch.zeros(l.out_features, dtype=W.dtype) for l in lins], 0)
-            whole = nn.Linear(W.shape[1], W.shape[0], bias=b is not None, dtype=torch.bfloat16)
-            whole.weight.data = W
-            if b is not None:
-                whole.bias.data = b
-            lin = NWCLinear(whole, device, elem=elem)
-            shared = {"lin": lin, "y": None, "x_id": None, "names": list(names), "sizes": [l.out_features for l in lins]}
-            a = 0
-            for i, (nm, l) in enumerate(zip(names, lins)):
-                setattr(mod, nm, _FusedHead(shared, i, a, a + l.out_features))
-                a += l.out_features
-                l.weight.data = torch.empty(0)
-            n_fused += 1
-    print(f"NWC: {n_fused} projection groups fused")
-    return n_fused
-
-
-def convert(model: nn.Module, device="cuda", verbose=True, tied=True, elem="bf16", embeddings=True):
-    """Replace every supported nn.Linear (and a tied embedding) by NWC modules; move the rest to `device`.
-    elem "bf16": lossless; "fp8": weight-only fp8 e4m3 (per-channel scale), the fp8 values stored lossless.
-    embeddings: also compress untied nn.Embedding tables (always lossless BF16, looked up with the gather kernel).
-    Returns (bytes_nwc, bytes_bf16) of the compressed matrices (nwc_torch.py:389-445)."""
-    total_nwc = total_bf16 = 0
-    replaced, skipped = 0, []
-    shared_ptrs = {m.weight.data_ptr() for m in model.modules() if isinstance(m, nn.Embedding)}
-    if tied:
-        embs = {m.weight.data_ptr(): m for m in model.modules() if isinstance(m, nn.Embedding)
-                and m.weight.dtype == torch.bfloat16 and fits(m.num_embeddings, m.embedding_dim)}
-        lins = [(name, mod, child, cm) for name, mod in list(model.named_modules()) for child, cm in list(mod.named_children())
-                if isinstance(cm, nn.Linear) and cm.weight.data_ptr() in embs]
-        for name, mod, child, cm in lins:
-            emb = embs[cm.weight.data_ptr()]
-            w = NWCWeight(emb.weight.data, device, elem=elem)
-            setattr(mod, child, NWCLinear(cm, device, w=w))
-            for ename, emod in list(model.named_modules()):
-                for echild, ecm in list(emod.named_children()):
-                    if ecm is emb:
-                        setattr(emod, echild, NWCEmbedding(emb, w))
-            total_nwc += w.bytes
-            total_bf16 += w.bytes_bf16
-            replaced += 1
-            shared_ptrs.discard(cm.weight.data_ptr())
-            emb.weight.data = torch.empty(0)
-            cm.weight.data = torch.empty(0)
-    if embeddings:
-        for name, mod in list(model.named_modules()):
-            for child, cm in list(mod.named_children()):
-                if isinstance(cm, nn.Embedding) and cm.weight.dtype == torch.bfloat16 and cm.weight.numel() \
-                        and fits(cm.num_embeddings, cm.embedding_dim):
-                    w = NWCWeight(cm.weight.data, device, elem="bf16")
-                    setattr(mod, child, NWCEmbedding(cm, w))
-                    total_nwc += w.bytes
-                    total_bf16 += w.bytes_bf16
-                    replaced += 1
-                    cm.weight.data = torch.empty(0)
-    for m in model.modules():
-        if isinstance(m, _FusedHead) and m.index == 0:
-            w = m.g["lin"].w
-            total_nwc += w.bytes
-            total_bf16 += w.bytes_bf16
-            replaced += 1
-    for name, mod in list(model.named_modules()):
-        for child, cm in list(mod.named_children()):
-            if isinstance(cm, nn.Linear) and cm.weight.dtype == torch.bfloat16 \
-                    and fits(cm.out_features, cm.in_features) and cm.weight.data_ptr() not in shared_ptrs:
-                new = NWCLinear(cm, device, elem=elem)
-                setattr(mod, child, new)
-                total_nwc += new.w.bytes
-                total_bf16 += new.w.bytes_bf16
-                replaced += 1
-                cm.weight.data = torch.empty(0)
-            elif isinstance(cm, nn.Linear):
-                reason = "tied" if cm.weight.data_ptr() in shared_ptrs else "shape"
-                skipped.append(f"{name}.{child} {tuple(cm.weight.shape)} [{reason}]")
-    model.to(device)
-    if verbose:
-        print(f"NWC ({elem}): {replaced} linear layers replaced, {total_bf16/1e9:.2f} GB BF16 -> {total_nwc/1e9:.2f} GB "
-              f"(ratio {total_nwc/max(total_bf16,1):.4f}" + (f", vs fp8 {total_nwc/max(total_bf16/2,1):.3f}" if elem == "fp8" else "") + ")")
-        if skipped:
-            print("  skipped:", ", ".join(skipped[:6]), "..." if len(skipped) > 6 else "")
-    return total_nwc, total_bf16
+        print(f"nwc_amd.convert_ref_fp8: {count} linear layers as uncompressed fp8")
+    return count

@@ -58,7 +58,7 @@ def test_save_load_roundtrip_cpu(tmp_path, tied):
         for names, parent in ((("q_proj", "k_proj", "v_proj"), f"model.layers.{i}.self_attn"),
                               (("gate_proj", "up_proj"), f"model.layers.{i}.mlp")):
             head = loaded.get_submodule(f"{parent}.{names[0]}")
-            w = head.g["lin"].w
+            w = head.group.lin.w
             dec = O.decode(oracle_encoding(w)).reshape(w.out_features, w.in_features)
             want = torch.cat([orig[f"{parent}.{n}.weight"] for n in names], 0)
             assert np.array_equal(dec, bits16(want))

@@ -249,7 +249,7 @@ def test_token_path_with_and_without_row_index(cuda, layout, M, K, split, escape
     ranges 4 or 8 long, and for K > 8192 several such items per half-wave) against the whole-block decode: o_proj, qkv_proj, gate_up and down shapes on 256 CUs,
     ragged matrices (layout 1: a last column block of three or two super-chunks), and escape runs (24-bit codes) dense
     enough ("heavy": three whole row groups) that tiles do not fit their LDS region and decode from global memory."""
-    from nwc_amd.nwc_torch import _lib, _ptr, _stream
+    from nwc_amd._abi import lib as _lib, ptr as _ptr, stream as _stream
     NWCWeight, _, _ = _nwc()
     w = bf16_matrix(M, K, seed=77, escapes=escapes == "sparse")
     if escapes == "dense":                    # 24-bit codes: whole lanes of rows 0-7, 9, 13 and 16-23 are escapes
@@ -318,7 +318,7 @@ def test_dequant_with_and_without_table(cuda, layout, M, K, escapes):
     original BF16 bits: a matrix wider than one round of blocks (K = 20000: 40 column blocks, the two-buffer kernel),
     gate_up and down of Qwen3-4B, and escape rows whose streams exceed their LDS region.  The token path on the wide
     matrix (one launch of the two-buffer kernel) against float64."""
-    from nwc_amd.nwc_torch import _lib, _ptr, _stream
+    from nwc_amd._abi import lib as _lib, ptr as _ptr, stream as _stream
     NWCWeight, _, _ = _nwc()
     print(f"dequant layout {layout} {M}x{K} {escapes}", flush=True)
     w = bf16_matrix(M, K, seed=M + K, escapes=False)
@@ -388,7 +388,7 @@ def test_reference_gather_shapes(cuda, layout, M, K):
     g = torch.Generator().manual_seed(2)
     ids = torch.cat([torch.tensor([0, M - 1, M // 2]), torch.randint(0, M, (61,), generator=g)])
     assert torch.equal(c.gather(ids.cuda()).cpu().view(torch.int16), w[ids].view(torch.int16))
-    from nwc_amd.nwc_torch import _lib, _ptr, _stream
+    from nwc_amd._abi import lib as _lib, ptr as _ptr, stream as _stream
     bad = torch.tensor([-1, M, 0, M + 7], dtype=torch.int64, device="cuda")
     out = torch.full((4, c.K16), 0x1234, dtype=torch.int16, device="cuda")
     assert _lib.nwc_gather(_stream(), _ptr(c.data), _ptr(c.bases), _ptr(c.hdr), _ptr(c.lut), _ptr(c.low), _ptr(bad), 4,
@@ -411,7 +411,7 @@ def test_random_shapes_all_paths(cuda, M, K, layout, elem):
     """Seeded random shapes through every path: dequant (bit-exact against the source for BF16; both entry points
     agree), gather, token path (BF16 x) within one BF16 ulp of float64 on the decoded weights (fp8: times the row
     scale), fp32 path within 1e-3."""
-    from nwc_amd.nwc_torch import _lib, _ptr, _stream
+    from nwc_amd._abi import lib as _lib, ptr as _ptr, stream as _stream
     NWCWeight, _, _ = _nwc()
     print(f"random shape {M}x{K} layout {layout} {elem}", flush=True)
     src = fp8_source(M, K, seed=M * 31 + K) if elem == "fp8" else bf16_matrix(M, K, seed=M * 31 + K)

@@ -17,7 +17,8 @@ FLAG = 1 << 30
 
 
 def _nwc():
-    from nwc_amd.nwc_torch import NWCWeight, _lib, _ptr, SEQ_TABLE_WORDS
+    from nwc_amd.nwc_torch import NWCWeight, SEQ_TABLE_WORDS
+    from nwc_amd._abi import lib as _lib, ptr as _ptr
     return NWCWeight, _lib, _ptr, SEQ_TABLE_WORDS
 
 
