@@ -68,11 +68,12 @@ def make_weight(M, K, seed):
 
 def clone_weight(c):
     """A second NWCWeight over distinct device buffers with the same content."""
+    import torch
     from nwc_amd.nwc_torch import NWCWeight
     d = NWCWeight.__new__(NWCWeight)
     d.__dict__.update(c.__dict__)
     for k in ("data", "bases", "hdr", "lut", "low", "_row_index"):
-        if getattr(c, k, None) is not None:
+        if isinstance(getattr(c, k, None), torch.Tensor):
             setattr(d, k, getattr(c, k).clone())
     return d
 

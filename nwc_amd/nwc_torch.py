@@ -56,8 +56,12 @@ def _need_gpu(t):
 # weight-only fp8
 
 def _absmax_scale(wf):
-    """Per-row fp32 scale: absmax / 448, with absmax floored at 1e-12 so all-zero rows divide safely."""
-    return wf.abs().amax(dim=1).clamp_min(1e-12) / FP8_MAX
+    """Per-row fp32 scale: absmax / 448, with absmax floored at 1e-12 so all-zero rows divide safely.  The divisor
+    is a tensor, not a Python number: torch on the GPU multiplies by the rounded reciprocal of a host scalar, which
+    is one ulp off the quotient for some rows, while a tensor divisor gives the correctly rounded quotient on every
+    device, as the CPU does."""
+    amax = wf.abs().amax(dim=1).clamp_min(1e-12)
+    return amax / torch.full_like(amax, FP8_MAX)
 
 
 def quantize_fp8(w: torch.Tensor):

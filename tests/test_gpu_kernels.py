@@ -265,7 +265,7 @@ def test_token_path_with_and_without_row_index(cuda, layout, M, K, split, escape
     assert _lib.nwc_token_split(c.n, K, c.code, 1) == split
     assert _lib.nwc_token_split(c.n, K, c.code, 0) == 1
     x = torch.randn(K, generator=torch.Generator().manual_seed(6)).to(torch.bfloat16).cuda()
-    xin = c._x16(x).contiguous()                             # zero-padded to K16 (layout 0) or K32 (layout 1)
+    xin = c._padded(x).contiguous()                             # zero-padded to K16 (layout 0) or K32 (layout 1)
     ys = []
     host = torch.zeros(c.seq_table().numel(), dtype=torch.int32)
     lut = c.lut.cpu()
