@@ -314,7 +314,8 @@ class NWCWeight:
         """x zero-extended to the kernels' width: K16 (layout 0) or in_features rounded up to 32 (layouts 1/2)."""
         width = -(-self.in_features // 32) * 32 if self.layout else self.K16
         extra = width - self.in_features
-        return (F.pad(x, (0, extra)) if extra else x).contiguous()
+        x = (F.pad(x, (0, extra)) if extra else x).contiguous()
+        return x if x.data_ptr() % 16 == 0 else x.clone()          # the kernels read x in 16-byte pieces
 
     def matvec(self, x_f32: torch.Tensor) -> torch.Tensor:
         """fp32 test path: y = W x in fp32 (times the row scale for fp8)."""

@@ -239,7 +239,7 @@ def test_row_index_values(cuda, M, K, escapes):
 @pytest.mark.parametrize("layout,M,K,split,escapes", [
     (0, 2560, 4096, 4, "none"), (0, 6144, 2560, 2, "none"), (0, 1003, 1100, 4, "none"), (0, 2560, 4096, 4, "sparse"),
     (0, 2560, 4096, 4, "dense"), (0, 6144, 2560, 2, "dense"), (0, 1003, 1100, 4, "dense"), (0, 2560, 4096, 4, "heavy"),
-    (0, 6144, 2560, 2, "heavy"),
+    (0, 6144, 2560, 2, "heavy"), (0, 19456, 2560, 1, "heavy"), (0, 2560, 9728, 1, "dense"), (0, 151936, 256, 1, "none"),
     (1, 2560, 4096, 4, "none"), (1, 6144, 2560, 4, "none"), (1, 19456, 2560, 2, "none"), (1, 1003, 1100, 4, "none"),
     (1, 2560, 4096, 4, "dense"), (1, 1003, 1100, 4, "dense"),
     (1, 2560, 9728, 4, "none"), (1, 2560, 9728, 4, "dense"), (1, 1003, 9000, 4, "none"), (1, 2560, 4096, 4, "heavy"),
@@ -280,6 +280,8 @@ def test_token_path_with_and_without_row_index(cuda, layout, M, K, split, escape
         assert err == 0
         ys.append(y.double().cpu().numpy())
     assert np.array_equal(ys[2], ys[0]) and np.array_equal(ys[3], ys[1])   # the table changes no sum: bit-identical
+    if layout == 0:                         # nor does layout 0's split: each row's lanes and blocks are summed in one order
+        assert np.array_equal(ys[0], ys[1])
     y64 = (w.cuda().double() @ x.double()).cpu().numpy()
     for y in ys:
         assert np.all(np.abs(y - y64) <= 2.0 ** -8 * np.abs(y64) + 1e-5)
