@@ -12,7 +12,10 @@ Reported: value = algorithmic bytes per token / GPU time per token (GB/s), with 
 36 copies' launches of one shape, and single launches between HIP events as the reference's kernbench does), the same
 sweep with hipBLASLt BF16 matvecs (F.linear), the roofline of the dominant kernel (the gate_up launch: algorithmic
 bytes / average launch time; HBM traffic from the committed counter summary profiles/traffic_gate_up.json) and the
-CPU baseline (the C oracle's decode + fp32 matvec of configs[0], on the host cores).
+CPU baseline (the C oracle's decode + fp32 matvec of configs[0], on the host cores).  Beside the sweep, and not in
+`value`: the vocabulary matrix that ends every token (Qwen3-4B: the tied 151936x2560 embedding used as lm_head), its
+launch time, and the per-token time of the sweep followed by it in one graph, as the reference's kernbench sums a
+token (36 layers x 4 + lm_head); --no-lm-head skips it.
 
 The other BASELINE configs, each printed as one JSON line of its own (not the driver's line):
   --config qwen3-0.6b      configs[1]: 28 layers of 4096x1024 / 1024x2048 / 6144x1024 / 1024x3072, BF16 layout 0
@@ -54,6 +57,10 @@ CONFIGS = {
     "qwen2.5-7b-l2": (28, [("qkv", 4608, 3584), ("o", 3584, 3584), ("gate_up", 37888, 3584), ("down", 3584, 18944)],
                       "bf16", 2, "Qwen2.5-7B-shaped 28-layer batch-1 token sweep, layout 2 (BASELINE configs[4])"),
 }
+# the vocabulary matrix each config's token ends with (Qwen3: the tied embedding; Qwen2.5-7B: the untied lm_head),
+# timed beside the sweep as the reference's per-token sum counts it (36 layers x 4 + lm_head)
+HEADS = {"qwen3-4b": (151936, 2560), "qwen3-0.6b": (151936, 1024), "qwen3-4b-fp8": (151936, 2560),
+         "qwen2.5-7b-l2": (152064, 3584)}
 
 
 def log(*a):
@@ -167,7 +174,7 @@ def timed_steps(step, steps, warmup):
     return e0.elapsed_time(e1) / steps
 
 
-def run_gpu(args, cfg):
+def run_gpu(args, cfg, head=None):
     import torch
     from nwc_amd.nwc_torch import NWCWeight, quantize_fp8, ref_fp8_matvec
     layers, shapes, elem, layout = cfg
@@ -191,9 +198,25 @@ def run_gpu(args, cfg):
     torch.cuda.synchronize()
     log(f"encoded + placed {len(shapes)}x{layers} compressed matrices in {time.time()-t0:.1f} s")
 
+    # the vocabulary matrix (one per token): two device copies alternate in the timings
+    if head is not None:
+        hM, hK = head
+        hw = make_weight(hM, hK, 1100)
+        hc = NWCWeight(hw, device=dev, layout=layout, elem=elem)
+        hx = torch.randn(hK, generator=torch.Generator().manual_seed(2100)).to(torch.bfloat16).to(dev)
+        base_head = ("lm_head", hM, hK, hc, hx, hw)
+        hcopies = [hc, clone_weight(hc)]
+        hys = [torch.empty(hM, dtype=torch.bfloat16, device=dev) for _ in hcopies]
+        hlaunch = [Launch(cc, hx, y) for cc, y in zip(hcopies, hys)]
+        torch.cuda.synchronize()
+        log(f"encoded + placed the {hM}x{hK} vocabulary matrix ({hc.bytes / 1e6:.1f} MB)")
+
     # correctness spot check of the last copies against a torch fp32 matvec on the decoded weights
-    for name, M, K, c, x, w in base:
-        y = copies[name][layers - 1].linear_bf16(x, None).float()
+    checks = [(name, M, K, copies[name][layers - 1], x) for name, M, K, c, x, w in base]
+    if head is not None:
+        checks.append(("lm_head", hM, hK, hcopies[1], hx))
+    for name, M, K, c, x in checks:
+        y = c.linear_bf16(x, None).float()
         wd = c.dequant().float()[:, :K]
         if c.scale is not None:
             wd = wd * c.scale[:, None]
@@ -201,6 +224,8 @@ def run_gpu(args, cfg):
         err = ((y - ref).abs() - (2 ** -8) * ref.abs()).max().item()
         if err > 1e-5:
             raise SystemExit(f"{name}: token path outside tolerance ({err:.3e})")
+    del wd, ref
+    torch.cuda.empty_cache()
 
     bytes_tok = sum(c.token_bytes() + 2 * K + 2 * M for name, M, K, c, x, w in base) * layers
     bf16_tok = sum(2 * M * K + 2 * K + 2 * M for name, M, K, *_ in base) * layers
@@ -233,6 +258,21 @@ def run_gpu(args, cfg):
     graph = graph_stack([sweep])
     ms_step = timed_steps(graph.replay if graph is not None else sweep, args.steps, args.warmup)
 
+    # ---- the vocabulary matrix: its own launch time, and the sweep followed by it as one graph per token ----
+    lm = None
+    if head is not None:
+        nb = hc.token_bytes() + 2 * hK + 2 * hM
+        h_ms = statistics.median(avg_launch_ms(lambda j: hlaunch[j % 2](cur()), 2, 4) for _ in range(5))
+
+        def sweep_head():
+            sweep()
+            hlaunch[0](cur())
+        hgraph = graph_stack([sweep_head])
+        ms_head = timed_steps(hgraph.replay if hgraph is not None else sweep_head, args.steps, args.warmup)
+        lm = {"M": hM, "K": hK, "nwc_bytes": hc.token_bytes(), "nwc_us": h_ms * 1e3, "nwc_GBps": nb / (h_ms * 1e-3) / 1e9,
+              "nwc_hbm_frac": nb / (h_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, "bytes": nb, "us_per_token_with_lm_head": ms_head * 1e3}
+        del hgraph
+
     # ---- hipBLASLt BF16 baseline: the same stack uncompressed ----
     blas = fp8 = None
     if not args.no_baseline:
@@ -260,6 +300,23 @@ def run_gpu(args, cfg):
                 "library": "torch F.linear, preferred_blas_library=hipblaslt"}
         del wcopy, bgraph
         torch.cuda.empty_cache()
+        if head is not None:
+            hW = [hw.to(dev) for _ in range(2)]
+            hxs = hx.view(1, hK)
+            g = graph_stack([(lambda j=j: F.linear(hxs, hW[j])) for j in range(2)])
+            h_us = timed_steps(g.replay, 4, 1) / 2 * 1e3
+
+            def bsweep_head():
+                bsweep()
+                F.linear(hxs, hW[0])
+            wcopy = {name: [w.to(dev) for _ in range(layers)] for name, M, K, c, x, w in base}
+            bhgraph = graph_stack([bsweep_head])
+            bhms = timed_steps(bhgraph.replay if bhgraph is not None else bsweep_head, args.steps, args.warmup)
+            blas["lm_head_us"] = h_us
+            blas["lm_head_GBps"] = (2 * hM * hK + 2 * hK + 2 * hM) / (h_us * 1e-6) / 1e9
+            blas["us_per_token_with_lm_head"] = bhms * 1e3
+            del g, bhgraph, hW, wcopy
+        torch.cuda.empty_cache()
         if elem == "fp8":
             # the library's uncompressed fp8 weight-only matvec on the same quantized weights (1 byte per weight)
             q8 = {}
@@ -284,7 +341,7 @@ def run_gpu(args, cfg):
     return {
         "ms_step": ms_step, "graph": graph is not None, "bytes_tok": bytes_tok, "bf16_tok": bf16_tok, "per": per,
         "sum_launch_us": sum_launch_us, "dom_bytes": dom_bytes, "dom_us": dom_ms * 1e3,
-        "achieved": dom_bytes / (dom_ms * 1e-3) / 1e9, "blas": blas, "fp8": fp8,
+        "achieved": dom_bytes / (dom_ms * 1e-3) / 1e9, "blas": blas, "fp8": fp8, "lm_head": lm,
         "device": {"name": props.name, "arch": props.gcnArchName, "cus": props.multi_processor_count},
     }
 
@@ -724,6 +781,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-baseline", action="store_true")
+    ap.add_argument("--no-lm-head", action="store_true", help="skip the vocabulary matrix's timings")
     ap.add_argument("--profile-launches", type=int, default=0,
                     help="only run the counter target (copies + this many gate_up launches), for rocprofv3 --pmc")
     ap.add_argument("--profile-shape", default=DOMINANT, choices=[s[0] for s in SHAPES],
@@ -757,7 +815,7 @@ def main():
 
     layers, shapes, elem, layout0, workload = CONFIGS[args.config]
     layout = args.layout if args.config in ("qwen3-4b", "qwen3-4b-fp8") else layout0
-    g = run_gpu(args, (layers, shapes, elem, layout))
+    g = run_gpu(args, (layers, shapes, elem, layout), None if args.no_lm_head else HEADS[args.config])
     cpu = None if args.no_cpu or args.config != "qwen3-4b" else run_cpu(args)
     us_tok = g["ms_step"] * 1e3
     value = g["bytes_tok"] / (g["ms_step"] * 1e-3) / 1e9
@@ -779,6 +837,18 @@ def main():
         "bytes_per_token": g["bytes_tok"], "bytes_per_token_bf16": g["bf16_tok"],
         "hbm_frac": round(value / PEAK_HBM_GBS, 4),
         "per_layer": [rnd(p) for p in g["per"]],
+        "lm_head": None if g["lm_head"] is None else rnd(g["lm_head"]),
+        "with_lm_head": None if g["lm_head"] is None else {
+            "us_per_token": round(g["lm_head"]["us_per_token_with_lm_head"], 1),
+            "bytes_per_token": g["bytes_tok"] + g["lm_head"]["bytes"],
+            "GBps": round((g["bytes_tok"] + g["lm_head"]["bytes"]) / g["lm_head"]["us_per_token_with_lm_head"] / 1e3, 1),
+            "hbm_frac": round((g["bytes_tok"] + g["lm_head"]["bytes"]) / g["lm_head"]["us_per_token_with_lm_head"] / 1e3
+                              / PEAK_HBM_GBS, 4),
+            "hipblaslt_us_per_token": None if blas is None else round(blas["us_per_token_with_lm_head"], 1),
+            "speedup_vs_hipblaslt": None if blas is None else round(blas["us_per_token_with_lm_head"] /
+                                                                     g["lm_head"]["us_per_token_with_lm_head"], 3),
+            "step": f"the {layers * len(shapes)} matvecs of the sweep + the {HEADS[args.config][0]}x"
+                    f"{HEADS[args.config][1]} vocabulary matvec, one HIP graph per token"},
         "hipblaslt": None if blas is None else rnd({**blas, "per_layer": [rnd(p) for p in blas["per_layer"]]}),
         "speedup_vs_hipblaslt": None if blas is None else round(blas["us_per_token_graph"] / us_tok, 3),
         "native_fp8": None if g["fp8"] is None else rnd(g["fp8"]),

@@ -46,10 +46,11 @@ constexpr uint32_t kDynLdsBudget = 48u * 1024u;       // dynamic LDS per workgro
 
 uint32_t slot_words_for(int layout) { return layout == 0 ? kSlotWords0 : layout == 1 ? kSlotWords1 : 0u; }
 
-// Layout 0: a workgroup owns G whole row groups, with G chosen so the grid is one residency round at two workgroups
-// per CU.  Tiles of at most 20 blocks get one half-wave per block (PIPE = false: every wave decodes at once, the most
-// latency hiding); larger tiles are spread evenly over at most 16 half-waves that each decode several blocks, one
-// round at a time, through two region buffers (PIPE = true).
+// Layout 0: a workgroup owns G whole row groups.  Where a tile of at most 32 blocks makes the grid one residency round
+// at two workgroups per CU, that G, with one half-wave (or, with the row index, two or four) per block; otherwise
+// tiles of at most 32 blocks over several rounds (PIPE = false: every wave decodes at once).  Only blocks of more than
+// 32 column blocks (K beyond 16384) are spread over at most 16 half-waves that each decode several blocks, one round
+// at a time, through two region buffers (PIPE = true).
 constexpr uint32_t kDynLdsPipe = 62u * 1024u;         // two such workgroups per CU next to their decode tables
 // A round buffer of 440 words per block holds the ~350-400 words of N(0, 0.02^2) or real-model BF16 blocks (a round
 // that does not fit decodes from global memory), so 32 blocks fit two workgroups per CU.
@@ -59,7 +60,7 @@ constexpr uint32_t kSlotWords2 = 440;
 // their dynamic LDS stays under this; the single-round tiers are tried with it first.
 constexpr uint32_t kDynLds13 = 47u * 1024u;
 
-bool plan_layout0_tiers(const Shape &f, int mode, int ncu, bool index, uint32_t budget, bool single_only, LaunchPlan &p);
+bool plan_layout0_tiers(const Shape &f, int mode, int ncu, bool index, uint32_t budget, bool no_pipe, LaunchPlan &p);
 bool plan_layout0(const Shape &f, int mode, int ncu, bool index, bool seq, LaunchPlan &p) {
     if (seq && (mode == kToken || mode == kDequant) && plan_layout0_tiers(f, mode, ncu, index, kDynLds13, true, p)) {
         p.seq13 = true;
@@ -68,7 +69,7 @@ bool plan_layout0(const Shape &f, int mode, int ncu, bool index, bool seq, Launc
     return plan_layout0_tiers(f, mode, ncu, index, kDynLdsPipe, false, p);
 }
 
-bool plan_layout0_tiers(const Shape &f, int mode, int ncu, bool index, uint32_t budget, bool single_only, LaunchPlan &p) {
+bool plan_layout0_tiers(const Shape &f, int mode, int ncu, bool index, uint32_t budget, bool no_pipe, LaunchPlan &p) {
     p = LaunchPlan{};
     p.layout = 0;
     const bool rows = mode == kToken || mode == kF32;
@@ -107,7 +108,19 @@ bool plan_layout0_tiers(const Shape &f, int mode, int ncu, bool index, uint32_t 
         const uint32_t lds = halves * kSlotWords2 * 4u + G * part;
         if (blocks <= 32u && lds <= budget) return set(false, 1u, G, halves, kSlotWords2, lds);
     }
-    if (single_only) return false;
+    // 2m. one block per half-wave over several residency rounds, when one round's tile would exceed 32 blocks: the
+    //     largest tile of at most 32 blocks whose LDS fits the budget (24 blocks next to the 13-bit table, 32 next to
+    //     the 12-bit one).  The rounds overlap one workgroup's stream copy with another's decode, which the pipelined
+    //     tier does inside one workgroup less well: 151936x2560 132.6 -> 104.6 us, 24576x4096 35.3 -> 27.8,
+    //     37888x3584 50.8 -> 40.7, 151936x4096 200.5 -> 152.9, 152064x3584 174.5 -> 143.8 (13-bit table).
+    if (CB <= 32u) {
+        for (uint32_t G = std::min(groups, 32u / CB); G >= 1u; G--) {
+            const uint32_t blocks = G * CB, halves = (blocks + 1u) & ~1u;
+            const uint32_t lds = halves * kSlotWords0 * 4u + G * part;
+            if (lds <= budget) return set(false, 1u, G, halves, kSlotWords0, lds);
+        }
+    }
+    if (no_pipe) return false;
     // 3. several blocks per half-wave: rounds through two region buffers, two workgroups per CU
     uint32_t G = std::max(1u, ceil_div(groups, 2u * ncu_));
     for (;; G--) {

@@ -313,13 +313,14 @@ def test_layout2_split_token_path(cuda, M, K, escapes):
 
 
 @pytest.mark.parametrize("layout,M,K,escapes", [
-    (0, 64, 20000, "none"), (0, 1003, 1100, "heavy"), (0, 19456, 2560, "none"), (0, 2560, 9728, "heavy"),
-    (1, 64, 20000, "none"), (1, 1003, 1100, "heavy"), (2, 1003, 1100, "none")])
+    (0, 64, 20000, "none"), (0, 4160, 16400, "none"), (0, 1003, 1100, "heavy"), (0, 19456, 2560, "none"),
+    (0, 2560, 9728, "heavy"), (1, 64, 20000, "none"), (1, 1003, 1100, "heavy"), (2, 1003, 1100, "none")])
 def test_dequant_with_and_without_table(cuda, layout, M, K, escapes):
     """nwc_dequant and nwc_dequant_seq (13-bit decode table for layouts 0/1, row index for layout 0) both return the
-    original BF16 bits: a matrix wider than one round of blocks (K = 20000: 40 column blocks, the two-buffer kernel),
-    gate_up and down of Qwen3-4B, and escape rows whose streams exceed their LDS region.  The token path on the wide
-    matrix (one launch of the two-buffer kernel) against float64."""
+    original BF16 bits: matrices wider than one round of blocks (K = 20000: 40 column blocks, the two-buffer kernel
+    with one row group per workgroup; 4160 x 16400: 33 column blocks, two row groups per workgroup), gate_up and down
+    of Qwen3-4B, and escape rows whose streams exceed their LDS region.  The token path on the wide matrices (the
+    two-buffer kernel) against float64."""
     from nwc_amd._abi import lib as _lib, ptr as _ptr, stream as _stream
     NWCWeight, _, _ = _nwc()
     print(f"dequant layout {layout} {M}x{K} {escapes}", flush=True)
