@@ -354,6 +354,7 @@ extern "C" int nwc_gather(void *stream, const uint8_t *data, const uint32_t *bas
 
 extern "C" int nwc_ref_fp8(void *stream, const uint8_t *w, const float *scale, const float *x, uint16_t *y, uint64_t M, uint32_t K) {
     if (M == 0 || K == 0 || M > 0xFFFFFFFFull) return -1;
-    if (current_cus() <= 0) return (int)hipErrorNoDevice;
-    return launch_ref_fp8(w, scale, x, y, (uint32_t)M, K, (hipStream_t)stream);
+    const int ncu = current_cus();
+    if (ncu <= 0) return (int)hipErrorNoDevice;
+    return launch_ref_fp8(w, scale, x, y, (uint32_t)M, K, ncu, (hipStream_t)stream);
 }
