@@ -665,31 +665,88 @@ def run_gather(args):
 
 
 def run_cpu(args):
-    """CPU baseline: the C oracle's decode + fp32 matvec of BASELINE configs[0] (9728 x 2560, layout 0, BF16) on all
-    host cores, repeated for about --cpu-seconds."""
+    """CPU baseline on BASELINE configs[0] (9728 x 2560 BF16, layout 0), each phase at 1 thread and on all host cores:
+    encode (the C oracle's single-threaded restatement of the reference encoder, nwc_ops.cu:245-320; all cores: the
+    library's multithreaded host encoder, byte-identical), decode (oracle, OpenMP over row groups), fp32 matvec on the
+    decoded BF16 weights (oracle), end-to-end decode + fp32 matvec (oracle, the reference's CPU path of
+    tests/test_format_cpu.py:36-111), and torch's CPU matvec for context (fp32 weights, and BF16).  Each phase repeats
+    for about --cpu-seconds / 10.  `value` is the end-to-end rate on all cores in compressed GB/s."""
     import numpy as np
     import torch
+    from nwc_amd._abi import lib as _lib, ptr as _ptr
+    from nwc_amd.nwc_torch import NPAIR, HDR_BLOCK, RAW_SLACK, _geometry
     from oracle import oracle as O
     cores = len(os.sched_getaffinity(0))
-    w = make_weight(9728, 2560, 7).view(torch.int16).numpy().view(np.uint16)
+    M, K = 9728, 2560
+    wt = make_weight(M, K, 7)
+    w = wt.view(torch.int16).numpy().view(np.uint16)
+    per = args.cpu_seconds / 10
+
+    def rate(fn, min_reps=2):
+        fn()                                                       # warm-up
+        reps, t0 = 0, time.perf_counter()
+        while True:
+            fn()
+            reps += 1
+            dt = time.perf_counter() - t0
+            if dt >= per and reps >= min_reps:
+                return dt / reps, reps
+
+    t0 = time.perf_counter()
     enc = O.encode(w, 0, 0)
-    x = torch.randn(2560, generator=torch.Generator().manual_seed(8)).to(torch.bfloat16).float().numpy()
+    t_enc1 = time.perf_counter() - t0
     nbytes = enc["dl"] + enc["bases"].size * 4 + enc["hdr"].size + 4096 * 4 + enc["n_low"]
-    y = O.linear(enc, x, threads=cores)                        # warm-up and check against the float64 closed form
+    x = torch.randn(K, generator=torch.Generator().manual_seed(8)).to(torch.bfloat16).float().numpy()
     y64 = O.bf16_to_f64(w) @ x.astype(np.float64)
-    assert np.all(np.abs(y - y64) <= 1e-3 * np.abs(y64) + 1e-5), "oracle CPU path outside tolerance"
-    reps, t0 = 0, time.perf_counter()
-    while True:
-        O.linear(enc, x, threads=cores)
-        reps += 1
-        dt = time.perf_counter() - t0
-        if dt >= args.cpu_seconds:
-            break
-    gbs = nbytes * reps / dt / 1e9
-    return {"value": round(gbs, 3), "unit": "GB/s", "cores": cores, "kind": "port",
-            "sample": f"configs[0]: 9728x2560 BF16 layout 0 ({nbytes/1e6:.1f} MB compressed), C oracle decode + fp32 matvec "
-                      f"(OpenMP over row groups), {reps} reps in {dt:.1f} s",
-            "us_per_matvec": round(dt / reps * 1e6, 1)}
+    for th in (1, cores):                                     # checks against the float64 closed form
+        assert np.array_equal(O.decode(enc, threads=th), w)
+        y = O.linear(enc, x, threads=th)
+        assert np.all(np.abs(y - y64) <= 1e-3 * np.abs(y64) + 1e-5), "oracle CPU path outside tolerance"
+
+    # the library's host encoder on all cores (byte-identical to the oracle's output)
+    src = wt.view(torch.int16).contiguous()
+    nb, n_low, _, _ = _geometry(M, K, 0)
+    cap = M * K + M * K // 2 + nb * 64 + 4096
+    bufs = dict(freq=torch.empty(NPAIR, dtype=torch.int16), psym=torch.empty(NPAIR, dtype=torch.int16),
+                bases=torch.empty(nb, dtype=torch.int32), hdr=torch.empty(nb * HDR_BLOCK, dtype=torch.uint8),
+                data=torch.empty(cap, dtype=torch.uint8), low=torch.zeros(n_low + RAW_SLACK, dtype=torch.uint8))
+    enc_lib = lambda: _lib.nwc_encode(_ptr(src), M * K, K, 0, _ptr(bufs["freq"]), _ptr(bufs["psym"]), _ptr(bufs["bases"]),
+                                      _ptr(bufs["hdr"]), _ptr(bufs["data"]), cap, _ptr(bufs["low"]))
+    assert enc_lib() == enc["dl"] and np.array_equal(bufs["data"].numpy()[:enc["dl"]], enc["data"][:enc["dl"]])
+    t_enc_all, _ = rate(enc_lib)
+
+    phases = {"encode": {"unit": "M weights/s", "threads_1": round(M * K / t_enc1 / 1e6, 1),
+                         f"threads_{cores}": round(M * K / t_enc_all / 1e6, 1),
+                         "note": "1 thread: the oracle's restatement of the reference encoder (one run); all cores: the "
+                                 "library's host encoder (nwc_encode), byte-identical"}}
+    dec = {}
+    for key, fn, nb_, unit in (
+            ("decode", lambda th: O.decode(enc, threads=th), nbytes, "compressed GB/s"),
+            ("fp32_matvec", lambda th: O.matvec_f32(w, x, threads=th), 2 * M * K, "BF16 GB/s"),
+            ("end_to_end", lambda th: O.linear(enc, x, threads=th), nbytes, "compressed GB/s")):
+        d = {"unit": unit}
+        for th in (1, cores):
+            t, reps = rate(lambda: fn(th))
+            d[f"threads_{th}"] = round(nb_ / t / 1e9, 3)
+            d[f"ms_threads_{th}"] = round(t * 1e3, 2)
+        phases[key] = d
+    nthreads = torch.get_num_threads()
+    wf32, xt = wt.float(), torch.from_numpy(x)
+    for key, W_, X_ in (("torch_fp32_matvec", wf32, xt), ("torch_bf16_matvec", wt, xt.to(torch.bfloat16))):
+        d = {"unit": "GB/s of the weights"}
+        for th in (1, cores):
+            torch.set_num_threads(th)
+            t, reps = rate(lambda: W_ @ X_)
+            d[f"threads_{th}"] = round(W_.numel() * W_.element_size() / t / 1e9, 3)
+            d[f"ms_threads_{th}"] = round(t * 1e3, 3)
+        phases[key] = d
+    torch.set_num_threads(nthreads)
+    e2e = phases["end_to_end"]
+    return {"value": e2e[f"threads_{cores}"], "unit": "GB/s", "cores": cores, "kind": "port",
+            "sample": f"configs[0]: 9728x2560 BF16 layout 0 ({nbytes/1e6:.1f} MB compressed); value = the C oracle's "
+                      f"decode + fp32 matvec on {cores} threads ({e2e[f'ms_threads_{cores}']} ms per matvec; "
+                      f"{e2e['ms_threads_1']} ms on 1 thread); each phase timed ~{per:.1f} s",
+            "us_per_matvec": round(e2e[f"ms_threads_{cores}"] * 1e3, 1), "phases": phases}
 
 
 def run_encode(args):

@@ -464,10 +464,15 @@ static int decode_group(const uint8_t *data, uint64_t dlen, const uint32_t *base
 }
 
 int or_decode(const uint8_t *data, uint64_t dlen, const uint32_t *bases, const uint8_t *hdr, const uint32_t *lut,
-              const uint8_t *low, uint64_t M, uint32_t K, int elem, uint16_t *out) {
+              const uint8_t *low, uint64_t M, uint32_t K, int elem, uint16_t *out, int threads) {
     if (M == 0 || K == 0 || M > 0xFFFFFFFFull) return -5;
     int lay = LAYOUT(elem);
     if (lay > 2 || TYPE(elem) > 1) return -5;
+#ifdef _OPENMP
+    if (threads > 0) omp_set_num_threads(threads);
+#else
+    (void)threads;
+#endif
     shape_t s = mk_shape((uint32_t)M, K, lay);
     int rc = 0;
     uint32_t ngroups = s.Mp / s.rows;

@@ -31,10 +31,10 @@ void or_build_tab(const uint16_t *psym, int elem, uint32_t *lut);
 
 /* Bit-serial decoder (test_format_cpu.py:36-111 for BF16; the fp8 assembly of nwc_ops.cu:418-442 / :836-879).
  * out = BF16 bits [M x K] (fp8: the unscaled fp8 value as BF16, exact).  Returns 0, or a negative code when the
- * stream is malformed: -1 read past data_len, -2 filler weight not coded as rank 0 / sign 0, -3 planes of a
+ * stream is malformed (OpenMP over row groups, `threads` of them when > 0): -1 read past data_len, -2 filler weight not coded as rank 0 / sign 0, -3 planes of a
  * filler or an exception not zero, -4 duplicate or unused exception entry, -5 bad shape. */
 int or_decode(const uint8_t *data, uint64_t data_len, const uint32_t *bases, const uint8_t *hdr, const uint32_t *lut,
-              const uint8_t *low, uint64_t M, uint32_t K, int elem, uint16_t *out);
+              const uint8_t *low, uint64_t M, uint32_t K, int elem, uint16_t *out, int threads);
 
 /* y[m] = sum_k bf16(w[m,k]) * x[k], fp32 accumulation in ascending k, OpenMP over rows (threads <= 0: all). */
 void or_matvec_f32(const uint16_t *w, uint64_t M, uint32_t K, const float *x, float *y, int threads);

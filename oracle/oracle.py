@@ -44,7 +44,7 @@ def lib():
         L.or_layout.restype = I; L.or_layout.argtypes = [U64, U32, I, P]
         L.or_encode.restype = ctypes.c_int64; L.or_encode.argtypes = [P, U64, U32, I, P, P, P, P, P, U64, P]
         L.or_build_tab.restype = None; L.or_build_tab.argtypes = [P, I, P]
-        L.or_decode.restype = I; L.or_decode.argtypes = [P, U64, P, P, P, P, U64, U32, I, P]
+        L.or_decode.restype = I; L.or_decode.argtypes = [P, U64, P, P, P, P, U64, U32, I, P, I]
         L.or_matvec_f32.restype = None; L.or_matvec_f32.argtypes = [P, U64, U32, P, P, I]
         L.or_linear.restype = I; L.or_linear.argtypes = [P, U64, P, P, P, P, U64, U32, I, P, P, P, I]
         L.or_f32_to_e4m3.restype = ctypes.c_uint8; L.or_f32_to_e4m3.argtypes = [ctypes.c_float]
@@ -106,12 +106,12 @@ def encode(w, elem=ELEM_BF16, layout=0, cap=None):
             "M": M, "K": K, "K16": K16, "nb": nb, "n_low": n_low, "n_scratch": n_scratch, "elem": elem, "layout": layout}
 
 
-def decode(enc):
-    """BF16 bits [M, K] (fp8: the unscaled fp8 values as BF16)."""
+def decode(enc, threads=0):
+    """BF16 bits [M, K] (fp8: the unscaled fp8 values as BF16); threads > 0 sets the OpenMP thread count."""
     M, K = enc["M"], enc["K"]
     out = np.zeros((M, K), np.uint16)
     rc = lib().or_decode(_p(enc["data"]), enc["data"].size, _p(enc["bases"]), _p(enc["hdr"]), _p(enc["lut"]),
-                         _p(enc["low"]), M, K, code(enc["elem"], enc["layout"]), _p(out))
+                         _p(enc["low"]), M, K, code(enc["elem"], enc["layout"]), _p(out), threads)
     if rc:
         raise ValueError(f"oracle decode: malformed stream ({rc})")
     return out
