@@ -86,28 +86,33 @@ bool plan_layout0_tiers(const Shape &f, int mode, int ncu, bool index, uint32_t 
         p.lds = lds;
         return true;
     };
-    // 1. small matrices with the row index: four or two half-waves per block (rows 0-1 / 2-3 / 4-5 / 6-7 or rows
-    //    0-3 / 4-7), up to 32 half-waves (16 waves) per workgroup, two workgroups per CU
-    // workgroups per CU: two, except where that leaves a workgroup four blocks or fewer (K <= 1024 matrices of up to
-    // 512 row groups): one, with twice the row groups, then stages its 32 KB decode table for twice the work
-    // (Qwen3-0.6B qkv 4096x1024 and gate_up 6144x1024: 11-12% faster)
-    const uint32_t wgpc = ceil_div(groups, 2u * ncu_) * CB <= 4u ? 1u : 2u;
-    if (index && (rows || mode == kDequant)) {
+    // One residency round, wgpc workgroups per CU of G = ceil(groups / (wgpc CUs)) row groups each:
+    // 1. with the row index, four or two half-waves per block (rows 0-1 / 2-3 / 4-5 / 6-7 or rows 0-3 / 4-7), up to
+    //    32 half-waves (16 waves) per workgroup; two per block only up to 20 half-waves when two workgroups share a CU;
+    // 2. else one half-wave per block, up to 32 blocks (the 58-VGPR kernel allows 8 waves per SIMD).
+    auto one_round = [&](uint32_t wgpc) {
         const uint32_t G = std::max(1u, ceil_div(groups, wgpc * ncu_)), blocks = G * CB;
-        const uint32_t lds = blocks * kSlotWords0 * 4u + G * part;
-        if (lds <= budget) {
-            if (4u * blocks <= 32u) return set(false, 4u, G, 4u * blocks, kSlotWords0, lds);
-            if (2u * blocks <= 20u) return set(false, 2u, G, 2u * blocks, kSlotWords0, lds);
+        if (index && (rows || mode == kDequant)) {
+            const uint32_t lds = blocks * kSlotWords0 * 4u + G * part;
+            if (lds <= budget) {
+                if (4u * blocks <= 32u) return set(false, 4u, G, 4u * blocks, kSlotWords0, lds);
+                if (2u * blocks <= (wgpc == 1u ? 32u : 20u)) return set(false, 2u, G, 2u * blocks, kSlotWords0, lds);
+            }
         }
-    }
-    // 2. one block per half-wave, one round: two workgroups of up to 32 half-waves (16 waves) per CU, which the
-    //    58-VGPR kernel allows (8 waves per SIMD)
-    {
-        const uint32_t G = std::max(1u, ceil_div(groups, wgpc * ncu_)), blocks = G * CB;
         const uint32_t halves = (blocks + 1u) & ~1u;
         const uint32_t lds = halves * kSlotWords2 * 4u + G * part;
-        if (blocks <= 32u && lds <= budget) return set(false, 1u, G, halves, kSlotWords2, lds);
-    }
+        return blocks <= 32u && lds <= budget && set(false, 1u, G, halves, kSlotWords2, lds);
+    };
+    // Workgroups per CU: one, with G1 = ceil(groups / CUs), when no CU then decodes more row groups than the busiest
+    // CU of the two-per-CU grid (G2 row groups per workgroup, ceil(groups / G2 / CUs) workgroups on it), or when two
+    // would leave a workgroup four blocks or fewer; a single workgroup stages its decode table once for the larger
+    // tile.  Qwen3-4B qkv (768 groups: 3 per CU instead of 2 x 2) 9.58 -> 8.88 us, o_proj (320 groups, G1 = 2, two
+    // half-waves per block) 8.44 -> 8.11, 9728x2560 (1216 groups: 5 instead of 2 x 3) 13.0 -> 11.2, Qwen3-0.6B qkv
+    // 4096x1024 and gate_up 6144x1024 11-12% faster.  Otherwise, or when that tile does not fit, two per CU.
+    const uint32_t G2 = std::max(1u, ceil_div(groups, 2u * ncu_)), G1 = ceil_div(groups, ncu_);
+    const uint32_t load2 = G2 * ceil_div(ceil_div(groups, G2), ncu_);
+    if ((G2 * CB <= 4u || G1 <= load2) && one_round(1u)) return true;
+    if (one_round(2u)) return true;
     // 2m. one block per half-wave over several residency rounds, when one round's tile would exceed 32 blocks: the
     //     largest tile of at most 32 blocks whose LDS fits the budget (24 blocks next to the 13-bit table, 32 next to
     //     the 12-bit one).  The rounds overlap one workgroup's stream copy with another's decode, which the pipelined
