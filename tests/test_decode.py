@@ -101,3 +101,46 @@ def test_greedy_token_is_first_argmax_cpu():
         assert int(bench.greedy_token(x)) == int(x.argmax()) == n // 3 if n > 1 else True
     x = torch.randint(0, 3, (151936,), generator=g).float()
     assert int(bench.greedy_token(x)) == int(x.argmax())
+
+
+@pytest.mark.gpu
+def test_graph_decode_nwc_matches_bf16_model(cuda):
+    """The converted model's HIP-graph decode against the uncompressed model's, both greedy from the same prompt on a
+    4-layer random-init Qwen3 with the Qwen3-0.6B layer shapes (hidden 1024, intermediate 3072, 16 heads, 8 KV heads)
+    and the 151936-token tied vocabulary.  The weights are bit-identical (lossless BF16); only the token path's
+    summation order differs from hipBLASLt's.  While the two token sequences agree, every step's logits must agree to
+    5% of their range, and the greedy token must agree wherever the uncompressed model's top-two margin exceeds twice
+    the largest logit difference seen so far."""
+    import nwc_amd
+    print("Qwen3-0.6B-shaped 4-layer graph decode, nwc vs bf16", flush=True)
+    cfg = dict(bench.QWEN3_ARCH["qwen3-0.6b"], num_hidden_layers=4)
+    ids = torch.randint(0, 151936, (1, 16), generator=torch.Generator().manual_seed(21)).cuda()
+    runs = {}
+    for mode in ("bf16", "nwc"):
+        model = bench.qwen3_model(cfg, seed=17, device="cuda")
+        if mode == "nwc":
+            nwc_amd.fuse(model, device="cuda")
+            nwc_amd.convert(model, device="cuda", verbose=False)
+        d = bench.GraphDecoder(model, ids, 24)
+        d.capture()
+        d.prefill()
+        logits = [d.logits.clone()]
+        for _ in range(24):
+            d.graph.replay()
+            logits.append(d.logits.clone())
+        torch.cuda.synchronize()
+        runs[mode] = (torch.stack(logits).cpu(), d.res[:25].cpu())
+        del d, model
+        torch.cuda.empty_cache()
+    (lb, tb), (ln, tn) = runs["bf16"], runs["nwc"]
+    worst = 0.0
+    for i in range(25):
+        if i > 0 and not torch.equal(tb[:i], tn[:i]):
+            break                                                 # the sequences differ from here on
+        diff = (ln[i] - lb[i]).abs().max().item()
+        worst = max(worst, diff)
+        assert diff <= 0.05 * (lb[i].max() - lb[i].min()).item(), f"step {i}"
+        top2 = lb[i].topk(2).values
+        if (top2[0] - top2[1]).item() > 2 * worst:
+            assert int(tn[i]) == int(tb[i]), f"step {i}"
+    print(f"steps compared: {i + 1 if torch.equal(tb, tn) else i}, largest logit difference {worst:.4f}", flush=True)
