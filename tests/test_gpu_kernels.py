@@ -243,7 +243,7 @@ def test_row_index_values(cuda, M, K, escapes):
     (1, 2560, 4096, 4, "none"), (1, 6144, 2560, 4, "none"), (1, 19456, 2560, 2, "none"), (1, 1003, 1100, 4, "none"),
     (1, 2560, 4096, 4, "dense"), (1, 1003, 1100, 4, "dense"),
     (1, 2560, 9728, 4, "none"), (1, 2560, 9728, 4, "dense"), (1, 1003, 9000, 4, "none"), (1, 2560, 4096, 4, "heavy"),
-    (1, 2560, 9728, 4, "heavy")])
+    (1, 2560, 9728, 4, "heavy"), (1, 151936, 2560, 2, "none")])
 def test_token_path_with_and_without_row_index(cuda, layout, M, K, split, escapes):
     """The split decode (layout 0: four or two half-waves per block, each reducing 2 or 4 rows; layout 1: super-chunk
     ranges 4 or 8 long, and for K > 8192 several such items per half-wave) against the whole-block decode: o_proj, qkv_proj, gate_up and down shapes on 256 CUs,
