@@ -342,6 +342,23 @@ def run_gpu(args, cfg, head=None):
                    "per_layer": fp8_per,
                    "library": "nwc_ref_fp8 (uncompressed fp8 e4m3 + fp32 row scale, 1 byte per weight; bandwidth-tuned "
                               "k_fp8_rows: every load of a wave's rows in flight at once)"}
+            if head is not None:                     # the vocabulary matrix through the same kernel, two copies
+                hq, hsc = quantize_fp8(hw)
+                hqs = [hq.to(dev) for _ in range(2)]
+                hsc, hxf = hsc.to(dev), hx.float()
+                h_us = avg_launch_ms(lambda j: ref_fp8_matvec(hqs[j % 2], hsc, hxf), 2, 8) * 1e3
+                hb = hM * hK + 4 * hM + 4 * hK + 2 * hM
+                fp8["lm_head_us"] = h_us
+                fp8["lm_head_GBps"] = hb / (h_us * 1e-6) / 1e9
+                fp8["lm_head_hbm_frac"] = fp8["lm_head_GBps"] / PEAK_HBM_GBS
+
+                def fsweep_head():
+                    fsweep()
+                    ref_fp8_matvec(hqs[0], hsc, hxf)
+                fhgraph = graph_stack([fsweep_head])
+                fp8["us_per_token_with_lm_head"] = timed_steps(fhgraph.replay if fhgraph is not None else fsweep_head,
+                                                               args.steps, args.warmup) * 1e3
+                del hqs, fhgraph
             del q8, fgraph
             torch.cuda.empty_cache()
 
@@ -910,6 +927,7 @@ def main():
             "hbm_frac": round((g["bytes_tok"] + g["lm_head"]["bytes"]) / g["lm_head"]["us_per_token_with_lm_head"] / 1e3
                               / PEAK_HBM_GBS, 4),
             "hipblaslt_us_per_token": None if blas is None else round(blas["us_per_token_with_lm_head"], 1),
+            "native_fp8_us_per_token": None if g["fp8"] is None else round(g["fp8"]["us_per_token_with_lm_head"], 1),
             "speedup_vs_hipblaslt": None if blas is None else round(blas["us_per_token_with_lm_head"] /
                                                                      g["lm_head"]["us_per_token_with_lm_head"], 3),
             "step": f"the {layers * len(shapes)} matvecs of the sweep + the {HEADS[args.config][0]}x"
