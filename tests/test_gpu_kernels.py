@@ -409,7 +409,19 @@ def _random_shapes(n, seed):
              int(g.integers(0, 3)), ["bf16", "fp8"][int(g.integers(0, 2))]) for _ in range(n)]
 
 
-@pytest.mark.parametrize("M,K,layout,elem", _random_shapes(24, 20261202))
+def _large_shapes(n, seed):
+    """Seeded tall shapes (30000-160000 rows, at most 2e8 weights) whose row groups do not fit one residency round:
+    the multi-round tiles of layouts 0 and 1 and layout 2's round-robin ranges."""
+    g = np.random.default_rng(seed)
+    out = []
+    for i in range(n):
+        M = int(np.exp(g.uniform(np.log(30000), np.log(160000))))
+        K = int(np.exp(g.uniform(np.log(256), np.log(min(6000, 2e8 / M)))))
+        out.append((M, K, i % 3, ["bf16", "fp8"][(i // 3) % 2]))
+    return out
+
+
+@pytest.mark.parametrize("M,K,layout,elem", _random_shapes(24, 20261202) + _large_shapes(6, 20261203))
 def test_random_shapes_all_paths(cuda, M, K, layout, elem):
     """Seeded random shapes through every path: dequant (bit-exact against the source for BF16; both entry points
     agree), gather, token path (BF16 x) within one BF16 ulp of float64 on the decoded weights (fp8: times the row
