@@ -60,16 +60,26 @@ constexpr uint32_t kSlotWords2 = 440;
 // their dynamic LDS stays under this; the single-round tiers are tried with it first.
 constexpr uint32_t kDynLds13 = 47u * 1024u;
 
-bool plan_layout0_tiers(const Shape &f, int mode, int ncu, bool index, uint32_t budget, bool no_pipe, LaunchPlan &p);
+// Planning stages, tried in this order for each decode table: one residency round, then several rounds of tiles of at
+// most 32 blocks, then (12-bit table only) the two-buffer kernel.  Every one-round plan, with either table, comes
+// before any multi-round plan.
+enum Stage { kOneRound, kRounds, kRoundsOrPipe };
+bool plan_layout0_tiers(const Shape &f, int mode, int ncu, bool index, uint32_t budget, Stage stage, LaunchPlan &p);
 bool plan_layout0(const Shape &f, int mode, int ncu, bool index, bool seq, LaunchPlan &p) {
-    if (seq && (mode == kToken || mode == kDequant) && plan_layout0_tiers(f, mode, ncu, index, kDynLds13, true, p)) {
+    const bool t13 = seq && (mode == kToken || mode == kDequant);
+    if (t13 && plan_layout0_tiers(f, mode, ncu, index, kDynLds13, kOneRound, p)) {
         p.seq13 = true;
         return true;
     }
-    return plan_layout0_tiers(f, mode, ncu, index, kDynLdsPipe, false, p);
+    if (plan_layout0_tiers(f, mode, ncu, index, kDynLdsPipe, kOneRound, p)) return true;
+    if (t13 && plan_layout0_tiers(f, mode, ncu, index, kDynLds13, kRounds, p)) {
+        p.seq13 = true;
+        return true;
+    }
+    return plan_layout0_tiers(f, mode, ncu, index, kDynLdsPipe, kRoundsOrPipe, p);
 }
 
-bool plan_layout0_tiers(const Shape &f, int mode, int ncu, bool index, uint32_t budget, bool no_pipe, LaunchPlan &p) {
+bool plan_layout0_tiers(const Shape &f, int mode, int ncu, bool index, uint32_t budget, Stage stage, LaunchPlan &p) {
     p = LaunchPlan{};
     p.layout = 0;
     const bool rows = mode == kToken || mode == kF32;
@@ -111,8 +121,7 @@ bool plan_layout0_tiers(const Shape &f, int mode, int ncu, bool index, uint32_t 
     // 4096x1024 and gate_up 6144x1024 11-12% faster.  Otherwise, or when that tile does not fit, two per CU.
     const uint32_t G2 = std::max(1u, ceil_div(groups, 2u * ncu_)), G1 = ceil_div(groups, ncu_);
     const uint32_t load2 = G2 * ceil_div(ceil_div(groups, G2), ncu_);
-    if ((G2 * CB <= 4u || G1 <= load2) && one_round(1u)) return true;
-    if (one_round(2u)) return true;
+    if (stage == kOneRound) return ((G2 * CB <= 4u || G1 <= load2) && one_round(1u)) || one_round(2u);
     // 2m. one block per half-wave over several residency rounds, when one round's tile would exceed 32 blocks: the
     //     largest tile of at most 32 blocks whose LDS fits the budget (24 blocks next to the 13-bit table, 32 next to
     //     the 12-bit one).  The rounds overlap one workgroup's stream copy with another's decode, which the pipelined
@@ -125,7 +134,7 @@ bool plan_layout0_tiers(const Shape &f, int mode, int ncu, bool index, uint32_t 
             if (lds <= budget) return set(false, 1u, G, halves, kSlotWords0, lds);
         }
     }
-    if (no_pipe) return false;
+    if (stage != kRoundsOrPipe) return false;
     // 3. several blocks per half-wave: rounds through two region buffers, two workgroups per CU
     uint32_t G = std::max(1u, ceil_div(groups, 2u * ncu_));
     for (;; G--) {
@@ -155,16 +164,21 @@ bool plan_layout0_tiers(const Shape &f, int mode, int ncu, bool index, uint32_t 
 constexpr uint32_t kSlotWords1s = 880, kSlotWords1Min = 768;
 constexpr uint32_t kDynLdsOne = 128u * 1024u;         // dynamic LDS of a workgroup that has its CU to itself
 constexpr uint32_t kDynLdsOne13 = 126u * 1024u;       // the same next to the 13-bit table
-bool plan_layout1_budget(const Shape &f, int mode, int ncu, bool index, uint32_t budget, uint32_t one, LaunchPlan &p);
+bool plan_layout1_budget(const Shape &f, int mode, int ncu, bool index, uint32_t budget, uint32_t one, Stage stage,
+                         LaunchPlan &p);
 bool plan_layout1(const Shape &f, int mode, int ncu, bool index, bool seq, LaunchPlan &p) {
-    if (seq && ((mode == kToken && index) || mode == kDequant) &&
-        plan_layout1_budget(f, mode, ncu, index, kDynLds13, kDynLdsOne13, p)) {
-        p.seq13 = true;
-        return true;
+    const bool t13 = seq && ((mode == kToken && index) || mode == kDequant);
+    for (Stage stage : {kOneRound, kRounds}) {
+        if (t13 && plan_layout1_budget(f, mode, ncu, index, kDynLds13, kDynLdsOne13, stage, p)) {
+            p.seq13 = true;
+            return true;
+        }
+        if (plan_layout1_budget(f, mode, ncu, index, kDynLdsPipe, kDynLdsOne, stage, p)) return true;
     }
-    return plan_layout1_budget(f, mode, ncu, index, kDynLdsPipe, kDynLdsOne, p);
+    return false;
 }
-bool plan_layout1_budget(const Shape &f, int mode, int ncu, bool index, uint32_t budget, uint32_t one, LaunchPlan &p) {
+bool plan_layout1_budget(const Shape &f, int mode, int ncu, bool index, uint32_t budget, uint32_t one, Stage stage,
+                         LaunchPlan &p) {
     p = LaunchPlan{};
     p.layout = 1;
     const bool rows = mode == kToken || mode == kF32;
@@ -189,6 +203,13 @@ bool plan_layout1_budget(const Shape &f, int mode, int ncu, bool index, uint32_t
         return false;
     };
     const uint32_t G1 = std::max(1u, (groups + 2u * (uint32_t)ncu - 1u) / (2u * (uint32_t)ncu));
+    if (stage == kRounds) {
+        // several residency rounds (the vocabulary matrices: 151936x2560 has 9496 groups): the largest tile that
+        // fits (151936x2560 token path, the row index now built as well: BF16 197.6 -> 113.5 us, fp8 237.1 -> 104.4)
+        for (uint32_t G = std::min(G1 - 1u, 32u / CB); G >= 1u; G--)
+            if (tile(G)) return true;
+        return false;
+    }
     if (tile(G1)) return true;
     // several items per half-wave: one 16-row group per workgroup, 32 half-waves, up to kDynLdsOne of LDS (one such
     // workgroup per CU; the region copy moves at most 64 KB)
@@ -206,10 +227,6 @@ bool plan_layout1_budget(const Shape &f, int mode, int ncu, bool index, uint32_t
             return true;
         }
     }
-    // several residency rounds (the vocabulary matrices: 151936x2560 has 9496 groups): the largest tile that fits
-    // (151936x2560 token path, the row index now built as well: BF16 197.6 -> 113.5 us, fp8 237.1 -> 104.4)
-    for (uint32_t G = std::min(G1 - 1u, 32u / CB); G >= 1u; G--)
-        if (tile(G)) return true;
     return false;
 }
 
