@@ -25,6 +25,8 @@ The other BASELINE configs, each printed as one JSON line of its own (not the dr
   --prefill 512            configs[2] prefill: per matrix, dequantization to a BF16 buffer + hipBLASLt GEMM of 512
                            tokens, against the GEMM on resident BF16 weights
   --gather 64              configs[4] embedding: 64 seeded ids from the 152064x3584 table, layouts 0, 1 and 2
+  --batch 4                configs[2] at 2..8 tokens: the batched fused kernel (no temporary buffer) against
+                           single-token launches, dequantization + hipBLASLt GEMM, and resident BF16
   --decode 128             model level: greedy decode of a random-init Qwen3 (--config qwen3-4b or qwen3-0.6b), one
                            HIP graph per token, BF16 (hipBLASLt) against NWC (--decode-elem bf16 or fp8)
   --encode                 the host encoder on configs[0] against the single-threaded oracle restatement (no GPU)
@@ -412,6 +414,69 @@ def run_prefill(args):
             "config": {"workload": "Qwen3-4B-shaped prefill (BASELINE configs[2]), 36 layers", "layout": args.layout,
                        "tokens": T},
             "per_stack": tot, "overhead_vs_resident": round(tot["dequant_gemm_us"] / tot["resident_bf16_us"], 3),
+            "per_layer": rows, "data": "synthetic N(0,0.02^2) BF16 weights, N(0,1) activations"}
+
+
+def run_batch(args):
+    """configs[2] at small batch: --batch T tokens through each 4B matrix (layout 0), the batched fused kernel (the
+    matrix decoded once per four tokens, no temporary buffer) against T single-token launches, the reference's path
+    for T > 1 (dequantization into a BF16 buffer + hipBLASLt GEMM) and the GEMM on resident BF16 weights; 8 copies
+    rotate so every launch reads HBM."""
+    import torch
+    import torch.nn.functional as F
+    from nwc_amd._abi import lib as _lib, ptr as _ptr
+    from nwc_amd.nwc_torch import NWCWeight
+    torch.backends.cuda.preferred_blas_library("hipblaslt")
+    dev = torch.device("cuda:0")
+    T, R = args.batch, 8
+    cur = lambda: ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    rows = []
+    for si, (name, M, K) in enumerate(SHAPES):
+        w = make_weight(M, K, 1000 + si)
+        c = NWCWeight(w, device=dev, layout=0)
+        cs = [c] + [clone_weight(c) for _ in range(R - 1)]
+        wb = [w.to(dev) for _ in range(R)]
+        tmp = torch.empty(M, c.K16, dtype=torch.bfloat16, device=dev)
+        X = torch.randn(T, K, generator=torch.Generator().manual_seed(3000 + si)).to(torch.bfloat16).to(dev)
+        Y = torch.empty(T, M, dtype=torch.bfloat16, device=dev)
+        ys = [torch.empty(M, dtype=torch.bfloat16, device=dev) for _ in range(T)]
+        singles = [[Launch(cc, X[t], ys[t]) for t in range(T)] for cc in cs]
+        got = cs[R - 1].linear_batch(X, None)
+        ref = torch.stack([cs[R - 1].linear_bf16(X[t], None) for t in range(T)])
+        if not torch.equal(got, ref):
+            raise SystemExit(f"{name}: batched token path differs from the single-token kernel")
+        args_b = []
+        for cc in cs:
+            st = cc.seq_table()
+            args_b.append([(_ptr(cc.data), _ptr(cc.bases), _ptr(cc.hdr), _ptr(cc.lut), _ptr(cc.low),
+                            _ptr(st) if st is not None else None, _ptr(X[t0]), None, None, _ptr(Y[t0]),
+                            ctypes.c_uint64(cc.n), ctypes.c_uint32(K), ctypes.c_int(cc.code), ctypes.c_uint32(min(4, T - t0)))
+                           for t0 in range(0, T, 4)])
+
+        def fused(j):
+            for a in args_b[j]:
+                if _lib.nwc_linear_xbf16_batch(cur(), *a):
+                    raise RuntimeError("nwc_linear_xbf16_batch failed")
+        t = {}
+        for key, fns in (("fused", [(lambda j=j: fused(j)) for j in range(R)]),
+                         ("single_token_launches", [(lambda j=j: [L(cur()) for L in singles[j]]) for j in range(R)]),
+                         ("dequant_gemm", [(lambda j=j: F.linear(X, cs[j].dequant(tmp)[:, :K])) for j in range(R)]),
+                         ("resident_bf16", [(lambda j=j: F.linear(X, wb[j])) for j in range(R)])):
+            g = graph_stack(fns)
+            t[key] = timed_steps(g.replay if g is not None else (lambda: [f() for f in fns]), 5, 2) / R * 1e3
+            del g
+        rows.append({"layer": name, "M": M, "K": K, "tokens": T, **{k + "_us": round(v, 2) for k, v in t.items()},
+                     "fused_GBps": round((c.token_bytes() + 2 * T * (K + M)) / (t["fused"] * 1e-6) / 1e9, 1)})
+        del cs, wb, tmp, singles
+        torch.cuda.empty_cache()
+    keys = ("fused_us", "single_token_launches_us", "dequant_gemm_us", "resident_bf16_us")
+    tot = {k: round(LAYERS * sum(r[k] for r in rows), 1) for k in keys}
+    return {"metric": f"{T}-token batch per Qwen3-4B stack: batched fused decode-matvec vs dequant + hipBLASLt GEMM",
+            "value": tot["fused_us"], "unit": "us", "higher_is_better": False, "dtype": "bf16",
+            "config": {"workload": "Qwen3-4B-shaped small batch (BASELINE configs[2]), 36 layers", "layout": 0,
+                       "tokens": T},
+            "per_stack": tot, "speedup_vs_dequant_gemm": round(tot["dequant_gemm_us"] / tot["fused_us"], 3),
+            "speedup_vs_single_token_launches": round(tot["single_token_launches_us"] / tot["fused_us"], 3),
             "per_layer": rows, "data": "synthetic N(0,0.02^2) BF16 weights, N(0,1) activations"}
 
 
@@ -871,6 +936,8 @@ def main():
     ap.add_argument("--config", default="qwen3-4b", choices=sorted(CONFIGS))
     ap.add_argument("--prefill", type=int, default=0, help="time the prefill path for this many tokens instead")
     ap.add_argument("--gather", type=int, default=0, help="time the embedding gather of this many ids instead")
+    ap.add_argument("--batch", type=int, default=0,
+                    help="time the batched token path for this many tokens (2..8) through each 4B matrix instead")
     ap.add_argument("--encode", action="store_true", help="time the host encoder on configs[0] (no GPU)")
     ap.add_argument("--decode-elem", default="bf16", choices=["bf16", "fp8"],
                     help="--decode: the NWC model's weights, lossless BF16 or weight-only fp8 (BASELINE configs[3])")
@@ -887,6 +954,9 @@ def main():
         return
     if args.prefill or args.gather:
         print(json.dumps(run_prefill(args) if args.prefill else run_gather(args)), flush=True)
+        return
+    if args.batch:
+        print(json.dumps(run_batch(args)), flush=True)
         return
     if args.decode:
         print(json.dumps(run_decode(args)), flush=True)

@@ -79,6 +79,17 @@ int nwc_linear_xbf16(void *stream, const uint8_t *data, const uint32_t *bases, c
                      const uint8_t *low, const uint16_t *row_index, const uint32_t *seq_table, const uint16_t *x,
                      const uint16_t *bias, const float *scale, uint16_t *y, uint64_t n, uint32_t K, int elem);
 
+/* Token path for ntok = 1..4 activation vectors at once, layout 0 (small batches): x BF16 [ntok][K16], y BF16
+ * [ntok][M], bias/scale as nwc_linear_bf16; seq_table as in nwc_linear_xbf16 (NULL: the stored 12-bit LUT).  Every
+ * decoded weight is multiplied into the ntok sums, so the matrix is decoded and read once for all of them; y[t] is
+ * bit-identical to nwc_linear_xbf16 on x[t].  -1 for layouts 1/2, ntok outside 1..4, or a matrix wider than
+ * 16384 columns.  No counterpart in the reference, whose Python side decompresses the whole matrix to a temporary
+ * BF16 buffer for any input of more than one token (nwc_torch.py:320-323). */
+int nwc_linear_xbf16_batch(void *stream, const uint8_t *data, const uint32_t *bases, const uint8_t *hdr,
+                           const uint32_t *tab, const uint8_t *low, const uint32_t *seq_table, const uint16_t *x,
+                           const uint16_t *bias, const float *scale, uint16_t *y, uint64_t n, uint32_t K, int elem,
+                           uint32_t ntok);
+
 /* Host: the 13-bit token-path decode table of layouts 0/1 from a stored LUT (host copy of `tab`): out[0..8191] one entry
  * per 13-bit window that starts with two complete codes ((17 - bits) | byte0 << 8 | byte1 << 16) or 0x40000000,
  * out[8192..8195] exp_of_rank[0..15].  Derived from the stored tensors once per matrix, not part of the format; 0,

@@ -155,6 +155,39 @@ bool plan_layout0_tiers(const Shape &f, int mode, int ncu, bool index, uint32_t 
     }
 }
 
+// Layout-0 token path for ntok activation vectors at once (k_layout0_batch): one half-wave per block, ntok partial
+// sums per row.  The one-round tile of the two-per-CU grid when it is small enough, else the largest such tile over
+// several rounds; at each stage the 13-bit table first (with `seq`), then the 12-bit LUT.
+bool plan_layout0_batch(const Shape &f, int ncu, uint32_t ntok, bool seq, LaunchPlan &p) {
+    const uint32_t CB = f.CB, groups = f.groups(), part = kRows0 * CB * 4u * ntok;
+    // blocks per tile that leave room for two workgroups per CU: the kernel takes 62-67 VGPRs for two vectors (7-8
+    // waves per SIMD), 71-75 for three (6), 87-88 for four (5)
+    const uint32_t cap = ntok <= 2u ? 32u : ntok == 3u ? 24u : 20u;
+    auto fit = [&](uint32_t G, uint32_t budget, uint32_t slot) {
+        const uint32_t blocks = G * CB, halves = (blocks + 1u) & ~1u, lds = halves * slot * 4u + G * part;
+        if (blocks > cap || lds > budget) return false;
+        p = LaunchPlan{};
+        p.layout = 0;
+        p.split = 1;
+        p.seq13 = budget == kDynLds13;
+        p.G = G;
+        p.threads = 32u * halves;
+        p.grid = (groups + G - 1u) / G;
+        p.slot_words = slot;
+        p.lds = lds;
+        return true;
+    };
+    const uint32_t G2 = std::max(1u, (groups + 2u * (uint32_t)ncu - 1u) / (2u * (uint32_t)ncu));
+    for (uint32_t budget : {kDynLds13, kDynLdsPipe})
+        if ((seq || budget != kDynLds13) && fit(G2, budget, kSlotWords2)) return true;
+    for (uint32_t budget : {kDynLds13, kDynLdsPipe}) {
+        if (!seq && budget == kDynLds13) continue;
+        for (uint32_t G = std::min(G2, cap / CB); G >= 1u; G--)
+            if (fit(G, budget, kSlotWords0)) return true;
+    }
+    return false;
+}
+
 // Layout 1, single round, for the token path and dequantization with the row index: G whole 16-row groups per
 // workgroup (two workgroups per CU), SP = 4 or 2 half-waves per block, at most 32 half-waves; a region buffer of up to
 // 880 words per block (a 16 x 512 block of N(0, 0.02^2) BF16 needs ~700, real model weights ~760).  Building the index
@@ -353,6 +386,23 @@ extern "C" int nwc_linear_xbf16(void *stream, const uint8_t *data, const uint32_
     if (!shape_ok(n, kBlock, K, elem)) return -1;
     return run_blocks(kToken, true, (hipStream_t)stream, data, bases, hdr, tab, low, x, bias, scale, y, n, K, elem,
                       elem_layout(elem) <= 1 ? row_index : nullptr, elem_layout(elem) <= 1 ? seq_table : nullptr);
+}
+
+extern "C" int nwc_linear_xbf16_batch(void *stream, const uint8_t *data, const uint32_t *bases, const uint8_t *hdr,
+                                      const uint32_t *tab, const uint8_t *low, const uint32_t *seq_table, const uint16_t *x,
+                                      const uint16_t *bias, const float *scale, uint16_t *y, uint64_t n, uint32_t K,
+                                      int elem, uint32_t ntok) {
+    if (!shape_ok(n, kBlock, K, elem) || elem_layout(elem) != 0 || ntok < 1 || ntok > 4) return -1;
+    if (ntok == 1)
+        return run_blocks(kToken, true, (hipStream_t)stream, data, bases, hdr, tab, low, x, bias, scale, y, n, K, elem,
+                          nullptr, seq_table);
+    const int ncu = current_cus();
+    if (ncu <= 0) return (int)hipErrorNoDevice;
+    const Shape f((uint32_t)(n / K), K, 0);
+    LaunchPlan p;
+    if (!plan_layout0_batch(f, ncu, ntok, seq_table != nullptr, p)) return -1;
+    BlockArgs a{data, bases, hdr, tab, low, x, bias, scale, y, nullptr, f.M, f.K, p.G, p.slot_words, seq_table};
+    return launch_layout0_batch(p, elem_type(elem), a, ntok, (hipStream_t)stream);
 }
 
 extern "C" int nwc_row_index(void *stream, const uint8_t *data, const uint32_t *bases, const uint8_t *hdr, const uint32_t *tab,

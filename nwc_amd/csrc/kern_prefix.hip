@@ -1058,6 +1058,137 @@ static int launch_prefix_t(const LaunchPlan &p, const BlockArgs &a, hipStream_t 
     return (int)hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------------------------------------------
+// Layout 0, token path for NT activation vectors at once (small batches: a few tokens, speculative drafts).  Tiles,
+// stream staging and the raw-row ring are those of k_layout0's single-round path with one half-wave per block (NR = 8);
+// every decoded weight pair goes through NT v_dot2, one per vector, so the NT products share one decode and one read
+// of the matrix.  x is BF16 [NT][K16], y BF16 [NT][M]; each vector's sums follow the single-vector kernel's order
+// exactly (lane order within a step, steps in order, the transposed half-wave reduction, column blocks ascending), so
+// y[t] is bit-identical to a single-vector launch on x[t].
+template <int ELEM, int NT, class Tab>
+__device__ __forceinline__ void row0_batch(Seq<ELEM> &S, const Tab &s, const uint4 &rw, const XRegs<true> (&x)[NT],
+                                           float (&sum)[NT]) {
+#pragma unroll
+    for (int t = 0; t < NT; t++) sum[t] = 0.f;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const uint32_t s0 = S.s;
+        const uint32_t *wp0 = S.wp;
+        uint32_t e1, e2;
+        if (__any(S.fast_quad(s, e1, e2) >= kSeqSlowTest)) {
+            S.s = s0;
+            S.wp = wp0;
+            S.reload();
+            S.slow_quad(s, e1, e2);
+        }
+        const uint32_t rk = u4_get(rw, k);
+        const uint32_t p0 = perm(e1, rk, kSelPair0), p1 = perm(e2, rk, kSelPair2);
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+            sum[t] = dot2_bf16(p0, x[t].b[2 * k], sum[t]);
+            sum[t] = dot2_bf16(p1, x[t].b[2 * k + 1], sum[t]);
+            asm volatile("" : "+v"(sum[t]));
+        }
+    }
+}
+
+// The eight rows of one block for NT vectors; `global`: the lane's stream read from memory (a round that does not fit
+// its LDS region), raw rows loaded as needed.  Returns, per vector, the row sums reduced as in rowsN (lane 4r: row r).
+template <int ELEM, int NT, bool GLOBAL, class Tab>
+__device__ __forceinline__ void rows_batch(const Tab &s, const uint32_t *lane, const BlockArgs &a, const Shape &f,
+                                           const XRegs<true> (&x)[NT], uint4 ring[kRing0], const Coord0 &c, uint32_t L,
+                                           float (&out)[NT]) {
+    Seq<ELEM> S;
+    S.init_at(lane, 0u);
+    float acc[NT][8];
+#pragma unroll
+    for (int r = 0; r < 8; r++) {
+        float sum[NT];
+        if constexpr (GLOBAL) {
+            row0_batch<ELEM, NT>(S, s, raw_row<ELEM>(a.low, f, c, r), x, sum);
+        } else {
+            row0_batch<ELEM, NT>(S, s, ring[r % kRing0], x, sum);
+            if (r + kRing0 < 8) ring[r % kRing0] = raw_row<ELEM>(a.low, f, c, r + kRing0);
+        }
+#pragma unroll
+        for (int t = 0; t < NT; t++) acc[t][r] = c.col_ok ? sum[t] : 0.f;
+    }
+#pragma unroll
+    for (int t = 0; t < NT; t++) out[t] = reduce8_transposed(acc[t], L);
+}
+
+template <int ELEM, int NT, int PEEK = kPeek>
+__global__ void __launch_bounds__(1024) k_layout0_batch(BlockArgs a) {
+    __shared__ LutT<PEEK> s;
+    extern __shared__ uint32_t dyn[];
+    const uint32_t tid = threadIdx.x, nth = blockDim.x, L = tid & 31, hw = tid >> 5, H = nth >> 5;
+    const uint32_t cap = a.slot_words * H;                    // one region slot per half-wave (one block each)
+    uint32_t *cur = dyn;
+    float *part = (float *)(dyn + cap);                       // [G * 8 rows][CB][NT]
+    const Shape f(a.M, a.K, 0);
+    const uint32_t rg0 = blockIdx.x * a.G;
+    const uint32_t ng = min(a.G, f.groups() - rg0);
+    const uint32_t nt = ng * f.CB, tl = nt - 1u;
+    const uint32_t B0 = rg0 * f.CB, nb = f.nb;
+    const uint32_t mend = B0 + nt == nb ? matrix_end(a, nb) : 0u;
+    const uint32_t t = hw;
+    const Coord0 c = coord0(min(t, tl), rg0, f, L);
+    const Region R = region_of(a, B0, B0 + min(H, nt), nb, mend);
+    TabStage<PEEK> Q;
+    Q.issue(a);
+    const uint32_t n = a.hdr[(uint64_t)c.b * kHdrBytes + L], base = a.bases[c.b];
+    Bulk Bk;
+    bulk_issue(Bk, a.data, R, tid, nth);
+    XRegs<true> x[NT];
+#pragma unroll
+    for (int v = 0; v < NT; v++) load_x16<true>(x[v], (const uint16_t *)a.x + (uint64_t)v * f.K16, c.col0, c.col_ok);
+    Q.commit(s, a);
+    uint4 ring[kRing0];
+#pragma unroll
+    for (int r = 0; r < kRing0; r++) ring[r] = raw_row<ELEM>(a.low, f, c, r);
+    const bool fits = R.n16 * 4u <= cap;
+    if (fits) bulk_commit(Bk, cur, R, tid, nth);
+    __syncthreads();
+    if (t < nt) {
+        const uint32_t start = c.col_ok ? half_scan_incl(n, L) - n : 0u;
+        float v[NT];
+        if (fits) rows_batch<ELEM, NT, false>(s, cur + ((base - R.lo16) >> 2) + start, a, f, x, ring, c, L, v);
+        else rows_batch<ELEM, NT, true>(s, (const uint32_t *)(a.data + base) + start, a, f, x, ring, c, L, v);
+        if ((L & 3u) == 0) {
+#pragma unroll
+            for (int u = 0; u < NT; u++) part[((c.g * kRows0 + (L >> 2)) * f.CB + c.cb) * NT + u] = v[u];
+        }
+    }
+    __syncthreads();
+    for (uint32_t i = threadIdx.x; i < ng * kRows0 * NT; i += blockDim.x) {
+        const uint32_t u = i % NT, rr = i / NT, row = rg0 * kRows0 + rr;
+        if (row >= a.M) continue;
+        float acc = 0.f;
+        for (uint32_t cb = 0; cb < f.CB; cb++) acc += part[(rr * f.CB + cb) * NT + u];
+        if (a.scale) acc *= a.scale[row];
+        if (a.bias) acc += __uint_as_float((uint32_t)a.bias[row] << 16);
+        ((uint16_t *)a.out)[(uint64_t)u * a.M + row] = (uint16_t)f32_to_bf16_rne(acc);
+    }
+}
+
+template <int ELEM, int PEEK>
+static int launch_batch_t(const LaunchPlan &p, const BlockArgs &a, uint32_t ntok, hipStream_t st) {
+    const dim3 g(p.grid), b(p.threads);
+    switch (ntok) {
+    case 2: hipLaunchKernelGGL((k_layout0_batch<ELEM, 2, PEEK>), g, b, p.lds, st, a); break;
+    case 3: hipLaunchKernelGGL((k_layout0_batch<ELEM, 3, PEEK>), g, b, p.lds, st, a); break;
+    case 4: hipLaunchKernelGGL((k_layout0_batch<ELEM, 4, PEEK>), g, b, p.lds, st, a); break;
+    default: return -1;
+    }
+    return (int)hipGetLastError();
+}
+
+int launch_layout0_batch(const LaunchPlan &p, int elem_t, const BlockArgs &a, uint32_t ntok, hipStream_t st) {
+    if (elem_t == kElemFp8)
+        return p.seq13 ? launch_batch_t<kElemFp8, kPeekSeq>(p, a, ntok, st) : launch_batch_t<kElemFp8, kPeek>(p, a, ntok, st);
+    return p.seq13 ? launch_batch_t<kElemBf16, kPeekSeq>(p, a, ntok, st) : launch_batch_t<kElemBf16, kPeek>(p, a, ntok, st);
+}
+
 int launch_prefix(const LaunchPlan &p, int elem_t, int mode, bool xbf16, const BlockArgs &a, hipStream_t st) {
     if (elem_t == kElemFp8) {
         if (mode == kDequant) return launch_prefix_t<kElemFp8, kDequant, true>(p, a, st);

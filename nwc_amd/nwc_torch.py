@@ -39,6 +39,10 @@ _default_layout = int(os.environ.get("NWC_LAYOUT", "0"))
 LAYOUT_DEFAULT = {ELEM_BF16: _default_layout, ELEM_FP8: _default_layout}
 SEQ_TABLE = os.environ.get("NWC_SEQ_TABLE", "1") != "0"   # layouts 0/1: stage the 13-bit decode table
 ROW_INDEX = os.environ.get("NWC_ROW_INDEX", "1") != "0"   # layouts 0/1: build the row index for the token path
+# layout 0: inputs of 2..BATCH_MAX tokens go through the fused kernel (four vectors per launch) instead of a
+# temporary BF16 matrix + F.linear
+BATCH_MAX = int(os.environ.get("NWC_BATCH_MAX", "8"))
+BATCH_LAUNCH = 4                                           # vectors per nwc_linear_xbf16_batch launch
 FP8_MAX = 448.0
 
 
@@ -342,6 +346,22 @@ class NWCWeight:
                  self.n, self.block, self.in_features, self.code)
         return y
 
+    def linear_batch(self, x: torch.Tensor, bias) -> torch.Tensor:
+        """Token path for a few BF16 vectors at once, layout 0: x [T, in_features] -> y BF16 [T, out_features], the
+        matrix decoded once per four vectors (y[t] equals linear_bf16(x[t]) bit for bit)."""
+        _need_gpu(self.data)
+        if self.layout != 0:
+            raise ValueError("linear_batch: layout 0 only")
+        T = x.shape[0]
+        xin = torch.zeros(T, self.K16, dtype=torch.bfloat16, device=x.device)
+        xin[:, :self.in_features] = x
+        y = torch.empty(T, self.out_features, dtype=torch.bfloat16, device=x.device)
+        for t0 in range(0, T, BATCH_LAUNCH):
+            nt = min(BATCH_LAUNCH, T - t0)
+            call("nwc_linear_xbf16_batch", stream(), *self._streams(), ptr(self.seq_table()), ptr(xin[t0]), ptr(bias),
+                 ptr(self.scale), ptr(y[t0]), self.n, self.in_features, self.code, nt)
+        return y
+
     def gather(self, ids: torch.Tensor) -> torch.Tensor:
         """Rows `ids` as BF16 [..., in_features], decoded straight from the compressed matrix (embedding lookup)."""
         _need_gpu(self.data)
@@ -385,7 +405,8 @@ def _bf16_bias(bias, device):
 
 class NWCLinear(nn.Module):
     """nn.Linear over a compressed matrix (elem "bf16" lossless, or "fp8" weight-only).  One BF16 token goes through
-    the fused decode-matvec kernel; anything else through a temporary BF16 matrix and F.linear."""
+    the fused decode-matvec kernel, up to NWC_BATCH_MAX (8) BF16 tokens of a layout-0 matrix through the batched one
+    (the matrix decoded once per four tokens); anything else through a temporary BF16 matrix and F.linear."""
 
     def __init__(self, linear: nn.Linear = None, device="cuda", block=None, w: "NWCWeight" = None, bias=None,
                  elem="bf16"):
@@ -402,6 +423,10 @@ class NWCLinear(nn.Module):
     def forward(self, x):
         if x.dtype == torch.bfloat16 and x.numel() == self.in_features:
             y = self.w.linear_bf16(x.contiguous().view(-1), self._bias_data())
+            return y.view(*x.shape[:-1], self.out_features)
+        tokens = x.numel() // self.in_features
+        if x.dtype == torch.bfloat16 and self.w.layout == 0 and 1 < tokens <= BATCH_MAX and self.w.K16 <= 16384:
+            y = self.w.linear_batch(x.reshape(tokens, self.in_features), self._bias_data())
             return y.view(*x.shape[:-1], self.out_features)
         weight = self.w.dequant()
         if self.w.scale is None:

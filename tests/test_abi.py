@@ -28,7 +28,7 @@ def _lib():
 def test_header_declares_the_reference_exports():
     d = _declared()
     assert REFERENCE_EXPORTS <= d
-    assert d - REFERENCE_EXPORTS == {"nwc_linear_xbf16", "nwc_row_index", "nwc_token_split",
+    assert d - REFERENCE_EXPORTS == {"nwc_linear_xbf16", "nwc_linear_xbf16_batch", "nwc_row_index", "nwc_token_split",
                                      "nwc_seq_table", "nwc_dequant_seq"}                                 # this build's additions
 
 
@@ -91,7 +91,16 @@ def _device_entry(lib):
     lib.nwc_matvec.argtypes = [P, P, P, P, P, P, P, P, U64, U32, U32, I]
     lib.nwc_linear_xbf16.restype = I
     lib.nwc_linear_xbf16.argtypes = [P, P, P, P, P, P, P, P, P, P, P, P, U64, U32, I]
+    lib.nwc_linear_xbf16_batch.restype = I
+    lib.nwc_linear_xbf16_batch.argtypes = [P, P, P, P, P, P, P, P, P, P, P, U64, U32, I, U32]
     return lib
+
+
+@pytest.mark.parametrize("elem,ntok", [(0x10, 2), (0x20, 2), (0x00, 0), (0x00, 5), (0x01, 9)])
+def test_batch_entry_point_refusals(elem, ntok):
+    """nwc_linear_xbf16_batch takes layout 0 and 1..4 vectors; anything else gets -1 before any device call."""
+    lib = _device_entry(_lib())
+    assert lib.nwc_linear_xbf16_batch(None, *([None] * 10), 2560 * 4096, 4096, elem, ntok) == -1
 
 
 @pytest.mark.parametrize("M,K,elem,ok", [
@@ -121,3 +130,4 @@ def test_device_entry_points_refuse_unaddressable_planes(M, K, elem, ok):
     assert lib.nwc_linear_bf16(None, *([None] * 10), n, 4096, K, elem) == -1
     assert lib.nwc_matvec(None, *([None] * 7), n, 4096, K, elem) == -1
     assert lib.nwc_linear_xbf16(None, *([None] * 11), n, K, elem) == -1
+    assert lib.nwc_linear_xbf16_batch(None, *([None] * 10), n, K, elem, 2) == -1
