@@ -160,9 +160,12 @@ bool plan_layout0_tiers(const Shape &f, int mode, int ncu, bool index, uint32_t 
 // several rounds; at each stage the 13-bit table first (with `seq`), then the 12-bit LUT.
 bool plan_layout0_batch(const Shape &f, int ncu, uint32_t ntok, bool seq, LaunchPlan &p) {
     const uint32_t CB = f.CB, groups = f.groups(), part = kRows0 * CB * 4u * ntok;
-    // blocks per tile that leave room for two workgroups per CU: the kernel takes 62-67 VGPRs for two vectors (7-8
-    // waves per SIMD), 71-75 for three (6), 87-88 for four (5)
-    const uint32_t cap = ntok <= 2u ? 32u : ntok == 3u ? 24u : 20u;
+    // blocks per tile (at least one row group's): the kernel takes 62-67 VGPRs for two vectors (7-8 waves per SIMD),
+    // 71-75 for three (6), 87-88 for four (5), so larger batches want smaller tiles; swept on MI355X (gate_up
+    // 19456x2560: three vectors 22.0 us at 20 blocks against 23.5-25.6 at 12-32, four 25.3 us at 15-16 against
+    // 30.2 at 20 and 27.0 at 25-32; qkv flat; down takes its whole 19-block row group)
+    if (CB > 32u) return false;
+    const uint32_t cap = std::max(CB, ntok <= 2u ? 32u : ntok == 3u ? 20u : 16u);
     auto fit = [&](uint32_t G, uint32_t budget, uint32_t slot) {
         const uint32_t blocks = G * CB, halves = (blocks + 1u) & ~1u, lds = halves * slot * 4u + G * part;
         if (blocks > cap || lds > budget) return false;
