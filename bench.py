@@ -35,6 +35,7 @@ usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--layout 0] [--cpu-
                                                  --profile-shape qkv|o|gate_up|down picks the matrix)
 """
 import argparse
+import contextlib
 import ctypes
 import json
 import os
@@ -659,7 +660,8 @@ def run_decode(args):
             orig = {k: v.detach().cpu().clone() for k, v in model.state_dict().items()
                     if v.dtype == torch.bfloat16 and v.dim() == 2}
             t0 = time.time()
-            fuse(model, device=dev, elem=args.decode_elem)
+            with contextlib.redirect_stdout(sys.stderr):        # stdout carries the one JSON line only
+                fuse(model, device=dev, elem=args.decode_elem)
             nwc_bytes, bf16_bytes = convert(model, device=dev, verbose=False, elem=args.decode_elem)
             torch.cuda.synchronize()
             log(f"decode: fuse + convert in {time.time() - t0:.1f} s, {nwc_bytes / 1e9:.2f} GB compressed of "
