@@ -3,8 +3,10 @@
 and the checkpoint round trip with logits compared bit for bit (reference tests/test_nwc_torch.py,
 tests/test_checkpoint.py:28-56, tests/test_fp8.py).
 
-Bars: token path within one BF16 ulp of a float64 matvec on the decoded weights (+1e-5); prefill equal to F.linear
-on the original weights (the same GEMM on bit-identical operands); decoded weights and gathered rows bit-exact;
+Bars: token path within one BF16 ulp of a float64 matvec on the decoded weights (+1e-5); 2-8 tokens of a layout-0
+matrix (the batched kernel) equal, token by token, to the single-token path; prefill (more tokens, or another layout)
+equal to F.linear on the original weights (the same GEMM on bit-identical operands); decoded weights and gathered rows
+bit-exact;
 model logits within 5% of the logit range of the uncompressed model (the reference doctor's bar, doctor.py:83)
 and bit-identical between a converted model and its reloaded checkpoint."""
 import numpy as np
@@ -47,7 +49,13 @@ def test_nwclinear_token_and_prefill(cuda, layout):
     err = np.abs(y1.double().cpu().numpy().ravel() - y64)
     assert np.all(err <= 2.0 ** -8 * np.abs(y64) + 1e-5)
     x5 = torch.randn(1, 5, K, generator=g).to(torch.bfloat16).cuda()
-    assert torch.equal(lin(x5), F.linear(x5, w.cuda(), b.cuda()))
+    y5 = lin(x5)
+    if layout == 0:                         # the batched kernel: each token as the single-token path computes it
+        assert torch.equal(y5, torch.cat([lin(x5[:, t:t + 1]) for t in range(5)], dim=1))
+    else:                                   # decompression + F.linear
+        assert torch.equal(y5, F.linear(x5, w.cuda(), b.cuda()))
+    x12 = torch.randn(1, 12, K, generator=g).to(torch.bfloat16).cuda()
+    assert torch.equal(lin(x12), F.linear(x12, w.cuda(), b.cuda()))
 
 
 @pytest.mark.parametrize("layout", [0, 1])
@@ -63,8 +71,11 @@ def test_nwclinear_fp8(cuda, layout):
     err = np.abs(lin(x1).double().cpu().numpy().ravel() - y64)
     assert np.all(err <= 2.0 ** -8 * np.abs(y64) + 1e-5)
     x3 = torch.randn(3, K, generator=g).to(torch.bfloat16).cuda()
-    want = (F.linear(x3, q.to(torch.bfloat16).cuda()).float() * scale.cuda()).to(torch.bfloat16)
-    assert torch.equal(lin(x3), want)
+    if layout == 0:                         # the batched kernel: each token as the single-token path computes it
+        assert torch.equal(lin(x3), torch.cat([lin(x3[t:t + 1]) for t in range(3)]))
+    x12 = torch.randn(12, K, generator=g).to(torch.bfloat16).cuda()
+    want = (F.linear(x12, q.to(torch.bfloat16).cuda()).float() * scale.cuda()).to(torch.bfloat16)
+    assert torch.equal(lin(x12), want)
 
 
 def test_embedding_gather(cuda):
