@@ -81,6 +81,16 @@ __device__ __forceinline__ uint4 raw_row(const uint8_t *__restrict__ low, const 
     return ldnt4(low + off);
 }
 
+// Bit position where part j (0-3) of block b starts in lane L's stream: 0 for the first part, else row-index entry
+// j - 1.  The entry is loaded for every part (the first part's load reads entry 0 and drops it): a load inside a branch
+// makes the compiler wait at the branch's end for it and for every request before it, which would hold back the
+// stream copy by a whole round trip.  Callers request it after their other prologue loads (the compiler may read its
+// register as the don't-care high half of a 64-bit multiply-add operand, which would wait for it).
+__device__ __forceinline__ uint32_t part_start(const BlockArgs &a, uint32_t b, uint32_t j, uint32_t L) {
+    const uint32_t v = a.aux[((uint64_t)b * kRowIndexSplits + (j ? j - 1u : 0u)) * kLanes + L];
+    return j ? v : 0u;
+}
+
 // Weights of one window step for the accumulator / dequant output.
 template <int MODE, bool XBF16>
 __device__ __forceinline__ void use_quad(uint32_t e1, uint32_t e2, uint32_t rk, int k, const XRegs<XBF16> &x, float &sum,
@@ -187,13 +197,14 @@ __device__ __forceinline__ float row0(Seq<ELEM, STRIDE> &S, const Tab &s, const 
     return sum;
 }
 
-// Raw rows in flight per half-wave: two.  The prologue then requests the streams and only rows 0-1, so decoding
-// starts sooner; each later row has one row's decode time to arrive (a deeper ring, or rows requested before the
-// streams, measured slower: the whole chip's first requests compete for HBM).
+// Raw rows in flight per half-wave: two.  The prologue requests rows 0-1 only once the wave's stream chunks have
+// arrived, so decoding starts sooner; each later row has one row's decode time to arrive (a deeper ring, or rows
+// requested together with the streams, measured slower: the whole chip's first requests compete for HBM, and the
+// workgroup waits for all of its streams).
 constexpr int kRing0 = 2;
 
 // Rows r0 .. r0 + NR - 1 of one layout-0 block for one lane, decoded from LDS starting at bit position P0 of the
-// lane's stream, with the first kRing0 of those raw-plane rows already requested into `ring`.  Returns the row sums
+// lane's stream, with the first kRing0 of those raw-plane rows already requested into `ring` (c.rb is row r0's offset).  Returns the row sums
 // reduced over the half-wave (NR = 8: lane 4r holds row r0 + r; NR = 4: lane 8r) or, for dequantization, stores the
 // rows; MODE kRowIndex records the row index (positions of rows 2, 4, 6) instead.  Fully unrolled: every row's raw
 // bytes live in their own registers.
@@ -210,7 +221,7 @@ __device__ __forceinline__ float rowsN(const Tab &s, const uint32_t *lane, uint3
         uint32_t pw[8];
         const float sum = row0<ELEM, MODE, XBF16>(S, s, ring[r % kRing0], x, pw);
         // eight rows go through a ring of kRing0 registers: row r + kRing0 is requested when row r is done
-        if (MODE != kRowIndex && r + kRing0 < NR) ring[r % kRing0] = raw_row<ELEM>(a.low, f, c, r0 + r + kRing0);
+        if (MODE != kRowIndex && r + kRing0 < NR) ring[r % kRing0] = raw_row<ELEM>(a.low, f, c, r + kRing0);
         if (MODE == kDequant) store_row0<MODE>(a, f, c.row0 + r0 + r, c.col0, c.col_ok, pw);
         else acc[r] = c.col_ok ? sum : 0.f;
     }
@@ -289,7 +300,7 @@ __device__ __forceinline__ float rowsN_global(const Tab &s, const uint32_t *lane
     for (int i = 0; i < NR; i++) acc[i] = 0.f;
 #pragma unroll 1
     for (int r = 0; r < NR; r++) {
-        const uint4 cur = raw_row<ELEM>(a.low, f, c, r0 + r);
+        const uint4 cur = raw_row<ELEM>(a.low, f, c, r);
         uint32_t pw[8];
         const float sum = row0<ELEM, MODE, XBF16>(S, s, cur, x, pw);
         if (MODE == kDequant) {
@@ -315,15 +326,19 @@ __device__ __forceinline__ float rowsN_global(const Tab &s, const uint32_t *lane
 //     waits on global memory.  One barrier per round publishes the next region.
 // Staging of the decode table: the stored 12-bit LUT, re-encoded (PEEK 12), or the prepared 13-bit table (PEEK 13).
 template <int PEEK> struct TabStage;
+// issue: the first chunks of the decode table; commit: store them; finish: the chunks a small workgroup has left,
+// called after every request that must not wait for the streams (lut_finish says why)
 template <> struct TabStage<kPeek> {
     LutLoad Q;
     __device__ __forceinline__ void issue(const BlockArgs &a) { lut_issue(Q, a.lut); }
-    __device__ __forceinline__ void commit(LutLds &s, const BlockArgs &a) { lut_commit<kLutSeq>(s, Q, a.lut); }
+    __device__ __forceinline__ void commit(LutLds &s) { lut_commit<kLutSeq>(s, Q); }
+    __device__ __forceinline__ void finish(LutLds &s, const BlockArgs &a) { lut_finish<kLutSeq>(s, a.lut); }
 };
 template <> struct TabStage<kPeekSeq> {
     SeqLoad Q;
     __device__ __forceinline__ void issue(const BlockArgs &a) { seq_issue(Q, a.seq); }
-    __device__ __forceinline__ void commit(LutLds13 &s, const BlockArgs &a) { seq_commit(s, Q, a.seq); }
+    __device__ __forceinline__ void commit(LutLds13 &s) { seq_commit(s, Q); }
+    __device__ __forceinline__ void finish(LutLds13 &s, const BlockArgs &a) { seq_finish(s, a.seq); }
 };
 
 template <int ELEM, int MODE, bool XBF16, bool PIPE, int NR, int PEEK = kPeek>
@@ -352,24 +367,34 @@ __global__ void __launch_bounds__(1024) k_layout0(BlockArgs a) {
     const uint32_t r0 = (hw % SP) * NR;                       // first row of this half-wave's share of the block
     Coord0 c = coord0(min(t, tl), rg0, f, L);
     Region R = region_of(a, B0, B0 + min(HB, nt), nb, mend);
+    if constexpr (!PIPE) {
+        // raw-plane offsets from this half-wave's first row on, computed before any vector load is requested: the
+        // compiler may use a register with a load in flight as the don't-care high half of a 64-bit multiply-add
+        // operand, and would then wait for that load.  (After the scalar loads of the region bounds: the empty asm
+        // counts as a memory write, which would turn later uniform loads into vector loads.)
+        c.rb += r0 * f.K16;
+        asm volatile("" : "+v"(c.rb));
+    }
     TabStage<PEEK> Q;
     Q.issue(a);
     uint32_t n = a.hdr[(uint64_t)c.b * kHdrBytes + L], base = a.bases[c.b];
-    const uint32_t P0 = r0 ? a.aux[((uint64_t)c.b * kRowIndexSplits + (r0 >> 1) - 1) * kLanes + L] : 0u;
     Bulk Bk;
     bulk_issue(Bk, a.data, R, tid, nth);
     XRegs<XBF16> x;
     if (ROWS) load_x16<XBF16>(x, a.x, c.col0, c.col_ok);
 
     if constexpr (!PIPE) {
-        // the table is stored before the raw rows are requested, so its registers are free for them
-        Q.commit(s, a);
+        // everything but the raw rows is requested before the first wait; rows 0-1 once this wave's stream chunks
+        // are in (requested together with the streams they delay them: o_proj 8.1 -> 8.7 us, qkv 9.1 -> 9.6)
+        const uint32_t P0 = NR == 8 ? 0u : part_start(a, c.b, r0 >> 1, L);
+        Q.commit(s);
+        Q.finish(s, a);
+        const bool fits = R.n16 * 4u <= cap;
+        if (fits) bulk_commit(Bk, cur, R, tid, nth);
         uint4 raw[kRing0];
 #pragma unroll
         for (int r = 0; r < (NR < kRing0 ? NR : kRing0); r++)
-            raw[r] = MODE == kRowIndex ? make_uint4(0u, 0u, 0u, 0u) : raw_row<ELEM>(a.low, f, c, r0 + r);
-        const bool fits = R.n16 * 4u <= cap;
-        if (fits) bulk_commit(Bk, cur, R, tid, nth);
+            raw[r] = MODE == kRowIndex ? make_uint4(0u, 0u, 0u, 0u) : raw_row<ELEM>(a.low, f, c, r);
         __syncthreads();
         if (t < nt) {
             const uint32_t start = c.col_ok ? half_scan_incl(n, L) - n : 0u;
@@ -388,7 +413,8 @@ __global__ void __launch_bounds__(1024) k_layout0(BlockArgs a) {
         Coord0 cn = coord0(min(t + H, tl), rg0, f, L);
         uint32_t n_n = a.hdr[(uint64_t)cn.b * kHdrBytes + L], base_n = a.bases[cn.b];
         Region Rn = region_of(a, B0 + min(H, tl), B0 + min(2u * H, nt), nb, mend);
-        Q.commit(s, a);
+        Q.commit(s);
+        Q.finish(s, a);
         if (R.n16 * 4u <= cap) bulk_commit(Bk, cur, R, tid, nth);
         __syncthreads();
         const uint32_t rounds = (nt + H - 1u) / H;
@@ -570,12 +596,22 @@ __device__ __forceinline__ uint4 x8_at(const void *x, uint32_t kc) {
 }
 // The activations are staged once per workgroup as BF16 in LDS, so their per-super-chunk reads are LDS reads: a global
 // load there would be waited for in issue order together with the raw chunks requested before it.
+// In three parts, as the decode table is staged: the first two chunks per thread are requested with the prologue's
+// other loads (x_issue) and stored after the table (x_commit; storing them waits for every load requested before
+// them, the streams included); x_finish copies the rest (fewer than n8 / 2 threads).
+template <bool XBF16> struct XStage { uint4 v0, v1; };
 template <bool XBF16>
-__device__ __forceinline__ void stage_x1(uint4 *xs, const void *x, uint32_t n8, uint32_t tid, uint32_t nth) {
-    const uint32_t i0 = tid, i1 = tid + nth;
-    const uint4 v0 = x8_at<XBF16>(x, 8u * min(i0, n8 - 1u)), v1 = x8_at<XBF16>(x, 8u * min(i1, n8 - 1u));
-    if (i0 < n8) xs[i0] = v0;
-    if (i1 < n8) xs[i1] = v1;
+__device__ __forceinline__ void x_issue(XStage<XBF16> &X, const void *x, uint32_t n8, uint32_t tid, uint32_t nth) {
+    X.v0 = x8_at<XBF16>(x, 8u * min(tid, n8 - 1u));
+    X.v1 = x8_at<XBF16>(x, 8u * min(tid + nth, n8 - 1u));
+}
+template <bool XBF16>
+__device__ __forceinline__ void x_commit(const XStage<XBF16> &X, uint4 *xs, uint32_t n8, uint32_t tid, uint32_t nth) {
+    if (tid < n8) xs[tid] = X.v0;
+    if (tid + nth < n8) xs[tid + nth] = X.v1;
+}
+template <bool XBF16>
+__device__ __forceinline__ void x_finish(uint4 *xs, const void *x, uint32_t n8, uint32_t tid, uint32_t nth) {
     for (uint32_t i = tid + 2u * nth; i < n8; i += nth) xs[i] = x8_at<XBF16>(x, 8u * i);
 }
 
@@ -730,14 +766,18 @@ __global__ void __launch_bounds__(1024) k_layout1s(BlockArgs a) {
     const uint32_t t = hw / SP, p = hw % SP, sc0 = p * NS;
     const Coord1 c = coord1<ELEM>(min(t, tl), rg0, f, L);
     const uint32_t n = a.hdr[(uint64_t)c.b * kHdrBytes + L], base = a.bases[c.b];
-    const uint32_t P0 = p ? a.aux[((uint64_t)c.b * kRowIndexSplits + sc0 / 4u - 1u) * kLanes + L] : 0u;
     Bulk Bk;
     bulk_issue(Bk, a.data, R, tid, nth);
-    if (ROWS) stage_x1<XBF16>(xs, a.x, n8, tid, nth);
-    Q.commit(s, a);
-    uint4 ring[4];
-#pragma unroll
-    for (int i = 0; i < kRing1; i++) ring[i] = MODE == kRowIndex ? make_uint4(0u, 0u, 0u, 0u) : raw1<ELEM>(a.low, c, sc0 + i);
+    XStage<XBF16> X;
+    if (ROWS) x_issue<XBF16>(X, a.x, n8, tid, nth);
+    // as in k_layout0: the raw chunks are requested once this wave's stream chunks are in
+    const uint32_t P0 = SP == 1 ? 0u : part_start(a, c.b, sc0 / 4u, L);
+    Q.commit(s);
+    if (ROWS) {
+        x_commit<XBF16>(X, xs, n8, tid, nth);
+        x_finish<XBF16>(xs, a.x, n8, tid, nth);
+    }
+    Q.finish(s, a);
     // the copy moves four 16-byte chunks per thread (512 words per half-wave); a larger region (one half-wave per
     // block, as when the row index is built) decodes from global memory, except for dequantization, which copies the
     // rest of its region in a second pass
@@ -748,6 +788,9 @@ __global__ void __launch_bounds__(1024) k_layout1s(BlockArgs a) {
             for (uint32_t i = tid + 4u * nth; i < R.n16; i += nth)
                 *(u32x4_t *)(cur + 4u * i) = *(const u32x4_t *)(a.data + R.lo16 + 16u * i);
     }
+    uint4 ring[4];
+#pragma unroll
+    for (int i = 0; i < kRing1; i++) ring[i] = MODE == kRowIndex ? make_uint4(0u, 0u, 0u, 0u) : raw1<ELEM>(a.low, c, sc0 + i);
     __syncthreads();
     if (t < nt) {
         const uint32_t start = half_scan_incl(n, L) - n;
@@ -805,8 +848,15 @@ __global__ void __launch_bounds__(1024) k_layout1m(BlockArgs a) {
     uint32_t P0 = p ? a.aux[(c.b * kRowIndexSplits + p - 1u) * kLanes + L] : 0u;
     Bulk Bk;
     bulk_issue(Bk, a.data, R, tid, nth);
-    stage_x1<true>(xs, a.x, n8, tid, nth);
-    Q.commit(s, a);
+    // the activations are stored first, which waits for the streams; then the table and the raw chunks (an order
+    // measured faster here than k_layout1s's: 2560x9728 15.8 us against 16.6-17.0, the later ones leaving the
+    // compiler a register choice that waits inside the item loop)
+    XStage<true> X;
+    x_issue<true>(X, a.x, n8, tid, nth);
+    x_commit<true>(X, xs, n8, tid, nth);
+    x_finish<true>(xs, a.x, n8, tid, nth);
+    Q.commit(s);
+    Q.finish(s, a);
     uint4 ring[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) ring[i] = raw1<ELEM>(a.low, c, p * NS + i);
@@ -1142,12 +1192,13 @@ __global__ void __launch_bounds__(1024) k_layout0_batch(BlockArgs a) {
     XRegs<true> x[NT];
 #pragma unroll
     for (int v = 0; v < NT; v++) load_x16<true>(x[v], (const uint16_t *)a.x + (uint64_t)v * f.K16, c.col0, c.col_ok);
-    Q.commit(s, a);
-    uint4 ring[kRing0];
-#pragma unroll
-    for (int r = 0; r < kRing0; r++) ring[r] = raw_row<ELEM>(a.low, f, c, r);
+    Q.commit(s);
+    Q.finish(s, a);
     const bool fits = R.n16 * 4u <= cap;
     if (fits) bulk_commit(Bk, cur, R, tid, nth);
+    uint4 ring[kRing0];                                         // once this wave's stream chunks are in
+#pragma unroll
+    for (int r = 0; r < kRing0; r++) ring[r] = raw_row<ELEM>(a.low, f, c, r);
     __syncthreads();
     if (t < nt) {
         const uint32_t start = c.col_ok ? half_scan_incl(n, L) - n : 0u;

@@ -141,9 +141,12 @@ __device__ __forceinline__ uint32_t lut_transform(uint32_t e) {
     return (e & 0xFFFFFF00u) | (KIND == kLutWindow ? ((32u - c) & 31u) : (18u - c));
 }
 
-// Table staging split in two so its loads overlap other requests: lut_issue reads the first 4 * blockDim 16-byte
+// Table staging in three parts so its loads overlap other requests: lut_issue reads the first 4 * blockDim 16-byte
 // chunks (all 1024 for >= 256 threads) and the word exp_of_rank[tid & 15] comes from; lut_commit re-encodes and
-// stores them (and any remaining chunks).  The caller publishes the table with a barrier.
+// stores them; lut_finish copies any remaining chunks (fewer than 256 threads).  A kernel calls lut_finish only after
+// every request that must not wait for the streams: the loads of its loop make the compiler wait for every
+// outstanding load where the loop ends, even when it runs no iteration.  The caller publishes the table with a
+// barrier.
 struct LutLoad {
     u32x4_t v0, v1, v2, v3;
     uint32_t ew;
@@ -168,22 +171,28 @@ __device__ __forceinline__ void lut_store4(LutLds &s, uint32_t i, u32x4_t e) {
     ((u32x4_t *)s.tab)[i] = e;
 }
 template <int KIND>
-__device__ __forceinline__ void lut_commit(LutLds &s, const LutLoad &Q, const uint32_t *__restrict__ lut) {
+__device__ __forceinline__ void lut_commit(LutLds &s, const LutLoad &Q) {
     const uint32_t tid = threadIdx.x, nth = blockDim.x;
     constexpr uint32_t n4 = kLutWords / 4;
     if (tid < n4) lut_store4<KIND>(s, tid, Q.v0);
     if (tid + nth < n4) lut_store4<KIND>(s, tid + nth, Q.v1);
     if (tid + 2u * nth < n4) lut_store4<KIND>(s, tid + 2u * nth, Q.v2);
     if (tid + 3u * nth < n4) lut_store4<KIND>(s, tid + 3u * nth, Q.v3);
-    for (uint32_t i = tid + 4u * nth; i < n4; i += nth) lut_store4<KIND>(s, i, ((const u32x4_t *)lut)[i]);   // < 256 threads
     const uint32_t q = tid & 15u;
     if (tid < 16) s.eor[tid] = q == 15u ? 0 : (uint8_t)((Q.ew >> ((q < 11u || (q & 1u)) ? 8u : 16u)) & 0x7Fu);
+}
+template <int KIND>
+__device__ __forceinline__ void lut_finish(LutLds &s, const uint32_t *__restrict__ lut) {
+    const uint32_t tid = threadIdx.x, nth = blockDim.x;
+    constexpr uint32_t n4 = kLutWords / 4;
+    for (uint32_t i = tid + 4u * nth; i < n4; i += nth) lut_store4<KIND>(s, i, ((const u32x4_t *)lut)[i]);   // < 256 threads
 }
 template <int KIND>
 __device__ __forceinline__ void stage_lut(LutLds &s, const uint32_t *__restrict__ lut) {
     LutLoad Q;
     lut_issue(Q, lut);
-    lut_commit<KIND>(s, Q, lut);
+    lut_commit<KIND>(s, Q);
+    lut_finish<KIND>(s, lut);
     __syncthreads();
 }
 
@@ -210,13 +219,17 @@ __device__ __forceinline__ void seq_store(LutLds13 &s, uint32_t i, u32x4_t v) {
     if (i < n4 - 1u) ((u32x4_t *)s.tab)[i] = v;
     else if (i == n4 - 1u) *(u32x4_t *)s.eor = v;                      // the last chunk: exp_of_rank
 }
-__device__ __forceinline__ void seq_commit(LutLds13 &s, const SeqLoad &Q, const uint32_t *__restrict__ tab) {
+__device__ __forceinline__ void seq_commit(LutLds13 &s, const SeqLoad &Q) {
     const uint32_t tid = threadIdx.x, nth = blockDim.x;
-    constexpr uint32_t n4 = kSeqTableWords / 4;
     seq_store(s, tid, Q.v0);
     seq_store(s, tid + nth, Q.v1);
     seq_store(s, tid + 2u * nth, Q.v2);
-    for (uint32_t i = tid + 3u * nth; i < n4; i += nth) seq_store(s, i, ((const u32x4_t *)tab)[i]);   // < 683 threads
+}
+// the chunks past the first three per thread (fewer than 683 threads); called as lut_finish is
+__device__ __forceinline__ void seq_finish(LutLds13 &s, const uint32_t *__restrict__ tab) {
+    const uint32_t tid = threadIdx.x, nth = blockDim.x;
+    constexpr uint32_t n4 = kSeqTableWords / 4;
+    for (uint32_t i = tid + 3u * nth; i < n4; i += nth) seq_store(s, i, ((const u32x4_t *)tab)[i]);
 }
 
 // ---- prefix-code window ----
