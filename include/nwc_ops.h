@@ -91,7 +91,7 @@ int nwc_linear_xbf16_batch(void *stream, const uint8_t *data, const uint32_t *ba
                            uint32_t ntok);
 
 /* Host: the 13-bit token-path decode table of layouts 0/1 from a stored LUT (host copy of `tab`): out[0..8191] one entry
- * per 13-bit window that starts with two complete codes ((17 - bits) | byte0 << 8 | byte1 << 16) or 0x40000000,
+ * per 13-bit window that starts with two complete codes ((16 - bits) | byte0 << 8 | byte1 << 16) or 0x40000000,
  * out[8192..8195] exp_of_rank[0..15].  Derived from the stored tensors once per matrix, not part of the format; 0,
  * or -1 for layout 2.  No counterpart in the reference. */
 int nwc_seq_table(const uint32_t *lut, int elem, uint32_t *out);

@@ -449,8 +449,9 @@ extern "C" void nwc_build_tab(const uint16_t *freq, const uint16_t *psym, int el
 }
 
 // Token-path decode table of layouts 0/1 with a 13-bit window, built from a stored LUT (its exp_of_rank): for every
-// 13-bit window that starts with two complete codes, (17 - c) | b0 << 8 | b1 << 16, the step encoding of the gfx950
-// kernel (byte 0 is the right shift that brings the second pair's 13 bits to [14:2]); for every other window the slow
+// 13-bit window that starts with two complete codes, (16 - c) | b0 << 8 | b1 << 16, the step encoding of the gfx950
+// kernel (byte 0 is the right shift that brings the second pair's 13 bits to [14:2] of its cursor's window, which
+// starts one bit before the next code); for every other window the slow
 // marker 0x40000000.  out[8192..8195] hold exp_of_rank[0..15] (the slow path's rank -> byte map).  Not part of the
 // format: a 13-bit window makes a pair too long for the table 3-4x rarer than the stored 12-bit LUT does (0.025%
 // instead of 0.087% of code pairs for N(0, 0.02^2) BF16), and each such pair costs its wave a code-by-code redo.
@@ -473,7 +474,7 @@ extern "C" int nwc_seq_table(const uint32_t *lut, int elem, uint32_t *out) {
             bytes[got++] = (sign << 7) | eor[z];
             start += z + 2;
         }
-        out[pat] = got == 2 ? (30u - P - start) | bytes[0] << 8 | bytes[1] << 16 : 0x40000000u;
+        out[pat] = got == 2 ? (29u - P - start) | bytes[0] << 8 | bytes[1] << 16 : 0x40000000u;
     }
     for (uint32_t j = 0; j < 4; j++)
         out[(1u << P) + j] = eor[4 * j] | (uint32_t)eor[4 * j + 1] << 8 | (uint32_t)eor[4 * j + 2] << 16 |

@@ -118,12 +118,11 @@ __device__ __forceinline__ float reduce2_transposed(float acc[2], uint32_t L) {
 // The stored 4096-word LUT is re-encoded once per workgroup.  For entries that are two complete codes byte 0 (c = bits
 // of both codes, 4..12) becomes
 //   kLutWindow: 32 - c, the funnel shift that advances a register window by c (Window);
-//   kLutSeq:    18 - c, the right shift that puts the second code pair's 12 bits at [13:2] (Seq); two entries added
-//               give 36 - (c1 + c2) in byte 0.
+//   kLutSeq:    17 - c, the right shift that puts the second code pair's 12 bits at [13:2] of the Seq cursor's
+//               window (which starts one bit early); two entries added give 34 - (c1 + c2) in byte 0.
 // Bytes 1/2 keep the two exponent bytes and byte 3 is 0.  The other entries (slow path) become: kLutWindow, the stored
-// entry with bit 31; kLutSeq, exactly kSeqSlow, so that a step's sum e1 + e2 + s - 36 is at least kSeqSlowTest when
-// either entry is slow and below it when both are fast (their bytes sum to less than 2^26; the only exception, an
-// all-zero pair of exponent bytes with a borrow out of byte 0, reads as slow and is merely redone).
+// entry with bit 31; kLutSeq, exactly kSeqSlow, so that a step's sum (Seq::fast_quad) is at least kSeqSlowTest when
+// either entry is slow and below it when both are fast (their bytes sum to less than 2^26).
 enum LutKind { kLutWindow = 0, kLutSeq = 1 };
 constexpr uint32_t kSeqSlow = 0x40000000u, kSeqSlowTest = 0x20000000u;
 
@@ -138,7 +137,7 @@ template <int KIND>
 __device__ __forceinline__ uint32_t lut_transform(uint32_t e) {
     if (e & kFlag) return KIND == kLutWindow ? e | 0x80000000u : kSeqSlow;
     const uint32_t c = e & 0xFFu;
-    return (e & 0xFFFFFF00u) | (KIND == kLutWindow ? ((32u - c) & 31u) : (18u - c));
+    return (e & 0xFFFFFF00u) | (KIND == kLutWindow ? ((32u - c) & 31u) : (29u - kPeek - c));
 }
 
 // Table staging in three parts so its loads overlap other requests: lut_issue reads the first 4 * blockDim 16-byte
@@ -312,11 +311,16 @@ struct Window {
 };
 
 // ---- bit cursor over an LDS-staged lane stream ----
-// P = bit position of the next code (0 = the MSB of the lane's word 0).  The cursor keeps the word pointer
-// wp = lane + ((P - 1) >> 5), the words A = wp[0], B = wp[1], C = wp[2], and s = 31 - ((P - 1) & 31): the 32 bits
-// from P are then alignbit(A, B, s).  An advance by c <= 24 bits moves at most one word, exactly when c > s:
-// A, B <- B, C, and the new C is read for the step after next, so no read of stream words lies on the dependency chain
-// of a step:  window -> table read (kLutSeq encoding) -> shift -> table read -> add -> test -> select -> window.
+// P = bit position of the next code (0 = the MSB of the lane's word 0).  The cursor works one bit behind it, at Q = P - 1:
+// it keeps the word pointer wp = lane + ((Q - 1) >> 5), the words A = wp[0], B = wp[1], C = wp[2], and a shift s with
+// s & 31 = 31 - ((Q - 1) & 31), so that the 32 bits from Q are alignbit(A, B, s): a don't-care bit (already consumed)
+// on top of the next 31.  s holds (s & 31) - 32 (bits 5-31 set; -32 is an inline constant of the instruction that
+// forms it).  Both choices serve one add: with table entries whose byte 0 is 29 - PEEK - c (16 - c for the 13-bit
+// table), e1 + e2 + s is (s & 31) - (c1 + c2) plus the exponent bytes' sums above byte 0, with no constant to add (a
+// cursor at P would need one).  An advance by c <= 24 bits moves at most one word, exactly
+// when that value is negative (bit 7): A, B <- B, C, and the new C is read for the step after next, so no read of
+// stream words lies on the dependency chain of a step:
+//   window -> table read (kLutSeq encoding) -> shift -> table read -> add -> test -> select -> window.
 // The words may live in LDS (staged streams) or global memory (fallback).  STRIDE is the distance in words between
 // consecutive words of a lane (1 for a lane stream stored contiguously; kLanes for 32 lanes interleaved word by word).
 template <int ELEM, int STRIDE = 1>
@@ -325,51 +329,54 @@ struct Seq {
     uint32_t s;
     uint32_t A, B, C;
 
-    // At P = 0, P - 1 = -1 lies in word -1, whose value is never used: shift 0 selects B, and any advance then moves
-    // a word.  It is not read either (word -1 of a global stream may precede the allocation).
+    // P = 0: Q - 1 = -2 lies in word -1 and s & 31 = 1, so A supplies only the window's don't-care top bit: it is set
+    // to 0 and word -1 is never read (in global memory it may precede the allocation).
     __device__ __forceinline__ void init(const uint32_t *lane) {
         wp = lane - STRIDE;
-        s = 0;
+        s = 1u | 0xFFFFFFE0u;
         A = 0u; B = lane[0]; C = lane[STRIDE];
     }
-    // start at bit position P of the lane's stream (any P >= 0; P = 0 is init's case)
+    // start at bit position P of the lane's stream (any P >= 0)
     __device__ __forceinline__ void init_at(const uint32_t *lane, uint32_t P) {
-        const int32_t m = (int32_t)P - 1;
+        const int32_t m = (int32_t)P - 2;
         wp = lane + (m >> 5) * STRIDE;
-        s = 31u - ((uint32_t)m & 31u);
+        s = (31u - ((uint32_t)m & 31u)) | 0xFFFFFFE0u;
         reload();
     }
     // the bit position of the next code
     __device__ __forceinline__ uint32_t position(const uint32_t *lane) const {
-        return (uint32_t)((wp - lane) / STRIDE) * 32u + 32u - s;
+        return (uint32_t)((wp - lane) / STRIDE) * 32u + 33u - (s & 31u);
     }
     __device__ __forceinline__ uint32_t window() const { return __builtin_amdgcn_alignbit(A, B, s); }
-    // t = s - c as an 8-bit two's complement value in its low byte (higher bits are don't-care); bit 7 says the
+    // t = (s & 31) - c as an 8-bit two's complement value in its low byte (higher bits are don't-care); bit 7 says the
     // cursor crossed into the next word
     __device__ __forceinline__ void step(uint32_t t) {
         const uint32_t x = __builtin_amdgcn_ubfe(t, 7, 1);
         const bool crossed = x != 0u;
-        s = t & 31u;
+        s = (t & 31u) | 0xFFFFFFE0u;
         A = crossed ? B : A;
         B = crossed ? C : B;
         wp += x * STRIDE;
         C = wp[2 * STRIDE];
     }
-    // re-read the cached words after the position was reset; A is dead when s = 0 (see init), so it is not read then
-    __device__ __forceinline__ void reload() { A = wp[s == 0 ? STRIDE : 0]; B = wp[STRIDE]; C = wp[2 * STRIDE]; }
+    // re-read the cached words after the position was reset.  A is dead when s & 31 = 0 and gives only the don't-care
+    // bit when s & 31 = 1, so it is read from wp[STRIDE] then (at P = 0, wp[0] is word -1)
+    __device__ __forceinline__ void reload() { A = wp[(s & 31u) <= 1u ? STRIDE : 0]; B = wp[STRIDE]; C = wp[2 * STRIDE]; }
 
     // Four codes = two pairs from two table reads; e1 holds the exponent bytes of weights 0,1 in bytes 1,2 and e2
-    // those of weights 2,3.  Byte 0 of e1 + e2 is 36 - c (kLutSeq), so t = e1 + e2 + s - 36 has s - c in its low byte
-    // (bytes 1-3 hold exponent sums and do not matter).  Returns t: the step is correct only if t < kSeqSlowTest;
-    // otherwise the caller resets the position and redoes the step with slow_quad.
-    // With a PEEK-bit table (12: the stored LUT re-encoded; 13: nwc_seq_table) byte 0 of an entry is 30 - PEEK - c.
+    // those of weights 2,3.  With a PEEK-bit table (13: nwc_seq_table; 12: the stored LUT re-encoded) byte 0 of an
+    // entry is 29 - PEEK - c, so e1 + e2 + s is (s & 31) - c + 2 (13 - PEEK) plus the exponent bytes' sums from byte 1
+    // on: the 13-bit table needs no constant, and the low byte is (s & 31) - c.  Returns t: the step is correct only
+    // if t < kSeqSlowTest (either entry slow: at least 2^30; both fast: below 2^26, except when all four exponent
+    // bytes are 0 and the low byte borrows, which reads as slow and is merely redone); otherwise the caller resets the
+    // position and redoes the step with slow_quad.
     template <int PEEK>
     __device__ __forceinline__ uint32_t fast_quad(const LutT<PEEK> &T, uint32_t &e1, uint32_t &e2) {
         constexpr uint32_t mask = ((1u << PEEK) - 1u) << 2;
         const uint32_t hi = window();
-        e1 = lds_entry(T, (hi >> (30 - PEEK)) & mask);
+        e1 = lds_entry(T, (hi >> (29 - PEEK)) & mask);
         e2 = lds_entry(T, (hi >> (e1 & 31u)) & mask);                  // the PEEK bits after the first c1
-        const uint32_t t = e1 + e2 + (s - 2u * (30u - PEEK));
+        const uint32_t t = PEEK == 13 ? e1 + e2 + s : e1 + e2 + s - 2u * (13u - PEEK);
         step(t);
         return t;
     }
@@ -377,7 +384,7 @@ struct Seq {
     // one code by counting leading zeros: rank r < max -> r zeros, one, sign; BF16 escape -> 15 zeros, one, byte
     template <int PEEK>
     __device__ __forceinline__ uint32_t slow_code(const LutT<PEEK> &T) {
-        const uint32_t hi = window();
+        const uint32_t hi = window() << 1;                             // the bits from P (codes take at most 24)
         uint32_t u = __clz((int)hi), b, c;
         if (ELEM == kElemFp8 || u < kMaxRankBf16) {
             u = u < 15u ? u : 15u;
@@ -387,7 +394,7 @@ struct Seq {
             b = (hi >> 8) & 0xFFu;
             c = 24u;
         }
-        step(s - c);
+        step((s & 31u) - c);
         return b;
     }
     template <int PEEK>

@@ -14,6 +14,7 @@ from tests.helpers import bf16_matrix, fp8_source
 
 SLOW = 0x40000000
 FLAG = 1 << 30
+BYTE0 = 16              # a fast entry's byte 0 is BYTE0 - c (c = bits of its two codes): the kernel's step encoding
 
 
 def _nwc():
@@ -49,14 +50,15 @@ def test_seq_table_agrees_with_stored_lut(elem, kind):
     t = _table(c)
     seq = t[:8192]
     fast = seq != SLOW
-    assert np.all((seq[fast] >> 24) == 0) and np.all((seq[fast] & 0xFF) >= 4) and np.all((seq[fast] & 0xFF) <= 13)
+    assert np.all((seq[fast] >> 24) == 0)
+    assert np.all((seq[fast] & 0xFF) >= BYTE0 - 13) and np.all((seq[fast] & 0xFF) <= BYTE0 - 4)   # 4 <= c <= 13
     p = np.arange(8192)
     e12 = lut[p >> 1]
     pair12 = (e12 & FLAG) == 0
     pair12[:4] = False                                   # patterns 0..3 map to entries 0/1 (exp_of_rank carriers)
     assert np.all(fast[pair12])
     assert np.array_equal(seq[pair12] & 0xFFFF00, e12[pair12] & 0xFFFF00)
-    assert np.array_equal(17 - (seq[pair12] & 0xFF), e12[pair12] & 0xFF)
+    assert np.array_equal(BYTE0 - (seq[pair12] & 0xFF), e12[pair12] & 0xFF)
     # the 13-bit table decodes strictly more windows: some pair is 13 bits long
     assert fast.sum() > pair12.sum()
     # exp_of_rank words: byte q is the symbol the stored LUT gives rank q with sign 0
@@ -92,11 +94,11 @@ def _decode_lanes(c, seq):
             while len(got) < 128:
                 e1 = int(seq[int(bits[pos:pos + 13], 2)])
                 if e1 != SLOW:
-                    c1 = 17 - (e1 & 0xFF)
+                    c1 = BYTE0 - (e1 & 0xFF)
                     e2 = int(seq[int(bits[pos + c1:pos + c1 + 13], 2)])
                     if e2 != SLOW:
                         got += [(e1 >> 8) & 0xFF, (e1 >> 16) & 0xFF, (e2 >> 8) & 0xFF, (e2 >> 16) & 0xFF]
-                        pos += c1 + 17 - (e2 & 0xFF)
+                        pos += c1 + BYTE0 - (e2 & 0xFF)
                         continue
                 for _ in range(4):                       # the slow path: four codes by the code definition
                     z = len(bits[pos:]) - len(bits[pos:].lstrip("0"))
