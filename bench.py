@@ -990,6 +990,8 @@ def main():
         "us_per_token_sum_of_launches": round(g["sum_launch_us"], 1),
         "bytes_per_token": g["bytes_tok"], "bytes_per_token_bf16": g["bf16_tok"],
         "hbm_frac": round(value / PEAK_HBM_GBS, 4),
+        # the uncompressed weights' bytes per token over the same time (the reference kernbench's "equivalent" column)
+        "bf16_equivalent_GBps": round(g["bf16_tok"] / (us_tok * 1e-6) / 1e9, 1),
         "per_layer": [rnd(p) for p in g["per"]],
         "lm_head": None if g["lm_head"] is None else rnd(g["lm_head"]),
         "with_lm_head": None if g["lm_head"] is None else {
