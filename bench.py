@@ -376,7 +376,9 @@ def run_gpu(args, cfg, head=None):
 
 def run_prefill(args):
     """configs[2] prefill: per 4B matrix, dequantization into a BF16 buffer + the hipBLASLt GEMM of --prefill tokens,
-    against the same GEMM on resident BF16 weights; 8 copies rotate so every launch reads HBM."""
+    against the same GEMM on resident BF16 weights, and (layout 0) the fused prefill kernel without the buffer
+    (nwc_prefill_xbf16, checked against float64 to the fp32-accumulation bound); 8 copies rotate so every launch
+    reads HBM."""
     import torch
     import torch.nn.functional as F
     from nwc_amd.nwc_torch import NWCWeight
@@ -395,11 +397,20 @@ def run_prefill(args):
         ref = F.linear(x, wb[0])
         if not torch.equal(y, ref):                 # same BF16 weights, same GEMM: identical outputs
             raise SystemExit(f"{name}: prefill through the compressed weights differs from the resident GEMM")
+        modes = [("dequant", [(lambda j=j: cs[j].dequant(tmp)) for j in range(R)]),
+                 ("gemm", [(lambda j=j: F.linear(x, tmp[:, :K])) for j in range(R)]),
+                 ("dequant_gemm", [(lambda j=j: F.linear(x, cs[j].dequant(tmp)[:, :K])) for j in range(R)]),
+                 ("resident_bf16", [(lambda j=j: F.linear(x, wb[j])) for j in range(R)])]
+        if args.layout == 0:
+            yf = cs[R - 1].prefill(x, None).double()
+            refd = x.double() @ w.to(dev).double().t()
+            bound = 2.0 ** -8 * refd.abs() + 2.0 ** -20 * (x.double().abs() @ w.to(dev).double().abs().t()) + 1e-6
+            if ((yf - refd).abs() > bound).any():
+                raise SystemExit(f"{name}: fused prefill outside the fp32-accumulation bound of float64")
+            del yf, refd, bound
+            modes.append(("fused", [(lambda j=j: cs[j].prefill(x, None)) for j in range(R)]))
         t = {}
-        for key, fns in (("dequant", [(lambda j=j: cs[j].dequant(tmp)) for j in range(R)]),
-                         ("gemm", [(lambda j=j: F.linear(x, tmp[:, :K])) for j in range(R)]),
-                         ("dequant_gemm", [(lambda j=j: F.linear(x, cs[j].dequant(tmp)[:, :K])) for j in range(R)]),
-                         ("resident_bf16", [(lambda j=j: F.linear(x, wb[j])) for j in range(R)])):
+        for key, fns in modes:
             g = graph_stack(fns)
             t[key] = timed_steps(g.replay if g is not None else (lambda: [f() for f in fns]), 5, 2) / R * 1e3
             del g
@@ -409,7 +420,8 @@ def run_prefill(args):
                      "gemm_TFLOPs": round(2 * T * M * K / (t["gemm"] * 1e-6) / 1e12, 1)})
         del cs, wb, tmp
         torch.cuda.empty_cache()
-    tot = {k: round(LAYERS * sum(r[k] for r in rows), 1) for k in ("dequant_us", "gemm_us", "dequant_gemm_us", "resident_bf16_us")}
+    keys = ("dequant_us", "gemm_us", "dequant_gemm_us", "resident_bf16_us") + (("fused_us",) if args.layout == 0 else ())
+    tot = {k: round(LAYERS * sum(r[k] for r in rows), 1) for k in keys}
     return {"metric": f"{args.prefill}-token prefill per Qwen3-4B stack: dequant to BF16 + hipBLASLt GEMM vs resident BF16 GEMM",
             "value": tot["dequant_gemm_us"], "unit": "us", "higher_is_better": False, "dtype": "bf16",
             "config": {"workload": "Qwen3-4B-shaped prefill (BASELINE configs[2]), 36 layers", "layout": args.layout,

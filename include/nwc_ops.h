@@ -90,6 +90,18 @@ int nwc_linear_xbf16_batch(void *stream, const uint8_t *data, const uint32_t *ba
                            const uint16_t *bias, const float *scale, uint16_t *y, uint64_t n, uint32_t K, int elem,
                            uint32_t ntok);
 
+/* Prefill of a layout-0 matrix for ntok >= 1 tokens without a temporary BF16 matrix: x BF16 [ntok][K16] (columns past
+ * K zero), y BF16 [ntok][M] = W x[t] (fp8: times scale) + bias, accumulated in fp32 on the matrix cores (summation order
+ * differs from a GEMM library's: results agree with F.linear on the decompressed weights to fp32 rounding, not bit for
+ * bit).  Each workgroup decodes 64 rows x 512 columns into LDS once per tile of up to 256 tokens.  row_index (from
+ * nwc_row_index) and seq_table (from nwc_seq_table) are required.  0 for ntok = 0; -1 for layouts 1/2, a missing
+ * row_index or seq_table, or ntok above 4194240.  Replaces the reference's prefill path, nwc_dequant into a temporary
+ * BF16 buffer + F.linear (nwc_torch.py:320-323, nwc_ops.cu:1121-1126); no counterpart export. */
+int nwc_prefill_xbf16(void *stream, const uint8_t *data, const uint32_t *bases, const uint8_t *hdr, const uint32_t *tab,
+                      const uint8_t *low, const uint16_t *row_index, const uint32_t *seq_table, const uint16_t *x,
+                      const uint16_t *bias, const float *scale, uint16_t *y, uint64_t n, uint32_t K, int elem,
+                      uint32_t ntok);
+
 /* Host: the 13-bit token-path decode table of layouts 0/1 from a stored LUT (host copy of `tab`): out[0..8191] one entry
  * per 13-bit window that starts with two complete codes ((16 - bits) | byte0 << 8 | byte1 << 16) or 0x40000000,
  * out[8192..8195] exp_of_rank[0..15].  Derived from the stored tensors once per matrix, not part of the format; 0,

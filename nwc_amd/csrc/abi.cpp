@@ -408,6 +408,31 @@ extern "C" int nwc_linear_xbf16_batch(void *stream, const uint8_t *data, const u
     return launch_layout0_batch(p, elem_type(elem), a, ntok, (hipStream_t)stream);
 }
 
+// Prefill (ntok >= 1 tokens) of a layout-0 matrix without a temporary BF16 matrix (k_prefill0).  Token tile: the
+// largest of 256, 128, 64 that the tokens need and that still gives the 64-row tiles at least one workgroup per CU
+// (each token tile decodes the matrix once more).
+uint32_t prefill_tokens_per_tile(uint32_t row_tiles, uint32_t ntok, int ncu) {
+    uint32_t tt = 256;
+    while (tt > 64u && (tt / 2u >= ntok || row_tiles * ((ntok + tt - 1u) / tt) < (uint32_t)ncu)) tt /= 2u;
+    return tt;
+}
+
+extern "C" int nwc_prefill_xbf16(void *stream, const uint8_t *data, const uint32_t *bases, const uint8_t *hdr,
+                                 const uint32_t *tab, const uint8_t *low, const uint16_t *row_index,
+                                 const uint32_t *seq_table, const uint16_t *x, const uint16_t *bias, const float *scale,
+                                 uint16_t *y, uint64_t n, uint32_t K, int elem, uint32_t ntok) {
+    if (!shape_ok(n, kBlock, K, elem) || elem_layout(elem) != 0 || !row_index || !seq_table) return -1;
+    if (ntok == 0) return 0;
+    if (ntok > 65535u * 64u) return -1;
+    const int ncu = current_cus();
+    if (ncu <= 0) return (int)hipErrorNoDevice;
+    const Shape f((uint32_t)(n / K), K, 0);
+    const uint32_t row_tiles = (f.groups() + 7u) / 8u;
+    PrefillArgs p{BlockArgs{data, bases, hdr, tab, low, nullptr, bias, scale, y, row_index, f.M, f.K, 8u, 0u, seq_table},
+                  x, ntok};
+    return launch_prefill0(elem_type(elem), prefill_tokens_per_tile(row_tiles, ntok, ncu), p, (hipStream_t)stream);
+}
+
 extern "C" int nwc_row_index(void *stream, const uint8_t *data, const uint32_t *bases, const uint8_t *hdr, const uint32_t *tab,
                              const uint8_t *low, uint16_t *row_index, uint64_t n, uint32_t K, int elem) {
     if (!shape_ok(n, kBlock, K, elem) || elem_layout(elem) > 1) return -1;

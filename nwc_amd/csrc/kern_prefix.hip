@@ -1268,4 +1268,241 @@ int launch_gather_prefix(int layout, int elem_t, const GatherArgs &a, hipStream_
     return (int)hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------------------------------------------
+// Prefill of a layout-0 matrix without a temporary BF16 copy: y[t] = W x[t] (+ bias, x scale) for T tokens.
+// A workgroup of 16 waves owns a tile of 64 rows (8 row groups) and TT tokens.  For each column block it decodes its
+// eight blocks into LDS as BF16 (wave 2j copies block j's streams; four half-waves then decode two rows each from the
+// row index's start, as dequantization does; lanes past K16 store zeros) and multiplies that 64 x 512 tile with the
+// activations of its TT tokens on the matrix cores: v_mfma_f32_16x16x32_bf16 with A = 16 rows x 32 columns of the tile
+// (one ds_read_b128 per lane: row lane & 15, columns 8 (lane >> 4) .. +7) and B = the same 32 columns of 16 tokens' x
+// (one 16-byte load per lane, two or four k-steps ahead), fp32 accumulators over the whole K.  Up to 256 tokens per
+// tile: more would not fit the accumulators next to the decode's registers without spilling.  The weights are decoded
+// once per token tile and nothing but y is written.
+constexpr uint32_t kPfRows = 64;                                 // rows per tile
+constexpr uint32_t kPfStride = 2u * kCols + 16u;                 // tile row stride in bytes: rows 4 banks apart
+constexpr uint32_t kPfSlot = 480;                                // stream words per block slot
+
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
+typedef __attribute__((ext_vector_type(4))) float f32x4_t;
+
+// waves of a TT-token tile: every wave covers the tile's 64 rows (four 16-row subtiles) and 16 tokens; TS waves along
+// the tokens, KS along the column block's 16 k-steps (each wave NK of them), so every activation is loaded once per
+// workgroup; the KS partial sums are added through LDS at the end
+template <int TT> struct PfShape {
+    static_assert(TT == 64 || TT == 128 || TT == 256, "64, 128 or 256 tokens per tile");
+    static constexpr int TS = TT / 16, KS = 16 / TS, NK = 16 / KS;
+    static constexpr int AHEAD = 2;                               // k-steps of activations in flight per wave
+};
+
+// A block's streams for its staging slot, two 16-byte chunks per lane of a wave (the slot holds kPfSlot words); the loads
+// are unconditional, at addresses clamped into the block's range.  start: the lane's word offset in the block; sh: the
+// block's offset in the slot; fits: whether the block fits the slot (else it decodes from global memory).
+__device__ __forceinline__ void pf_stage_issue(const BlockArgs &a, uint32_t n, uint32_t base, uint32_t L, uint32_t lane,
+                                               uint4 &v0, uint4 &v1, uint32_t &start, uint32_t &sh, bool &fits) {
+    const uint32_t incl = half_scan_incl(n, L), total = __shfl(incl, 31, 32);
+    start = incl - n;
+    sh = (base & 15u) >> 2;
+    const uint32_t need = sh + total + 3u;
+    fits = need <= kPfSlot;
+    const uint8_t *src = a.data + (base & ~15u);
+    const uint32_t last = ((min(need, kPfSlot) - 1u) & ~3u) * 4u;     // bytes; inside the block's range
+    v0 = *(const uint4 *)(src + min(16u * lane, last));
+    v1 = *(const uint4 *)(src + min(16u * lane + 1024u, last));
+}
+__device__ __forceinline__ void pf_stage_commit(uint32_t *slot, uint32_t lane, const uint4 &v0, const uint4 &v1) {
+    *(uint4 *)(slot + 4u * lane) = v0;
+    if (4u * lane + 256u < kPfSlot) *(uint4 *)(slot + 4u * lane + 256u) = v1;
+}
+
+// two rows of a block for one lane from bit position P0 (separate call sites keep LDS and global reads apart)
+template <int ELEM>
+__device__ __forceinline__ void pf_rows(const LutLds13 &s, const uint32_t *lane, uint32_t P0, const uint4 (&raw)[2],
+                                        const XRegs<true> &xnone, uint32_t (&pw)[2][8]) {
+    Seq<ELEM> S;
+    S.init_at(lane, P0);
+#pragma unroll
+    for (int r = 0; r < 2; r++) {
+        row0<ELEM, kDequant, true>(S, s, raw[r], xnone, pw[r]);
+        asm volatile("" : "+v"(pw[r][0]), "+v"(pw[r][7]));
+    }
+}
+
+template <int ELEM, int TT>
+__global__ void __launch_bounds__(1024) k_prefill0(PrefillArgs p) {
+    using PS = PfShape<TT>;
+    constexpr int WR = 4, TS = PS::TS, KS = PS::KS, NK = PS::NK, AH = PS::AHEAD;
+    const BlockArgs &a = p.a;
+    __shared__ LutT<kPeekSeq> s;
+    extern __shared__ uint32_t dyn[];
+    uint8_t *tile = (uint8_t *)dyn;
+    uint32_t *slots = (uint32_t *)(tile + kPfRows * kPfStride);
+    const uint32_t tid = threadIdx.x, L = tid & 31, lane = tid & 63, wv = tid >> 6, hw = tid >> 5;
+    const Shape f(a.M, a.K, 0);
+    const uint32_t rg0 = blockIdx.x * (kPfRows / kRows0), groups = f.groups(), CB = f.CB;
+    // decode role: half-wave hw decodes rows 2q, 2q + 1 of tile block j (row group rg0 + j) of every column block; a
+    // tile past the matrix's last row group decodes that group again into rows that are never stored.  Wave 2j stages
+    // block j's streams.
+    const uint32_t j = hw >> 2, q = hw & 3, jj = min(rg0 + j, groups - 1u) - rg0;
+    const bool copier = (wv & 1u) == 0u;
+    uint32_t *slot = slots + j * kPfSlot;
+    // matrix-core role: the tile's 64 rows, tokens tok0 .. + 15, k-steps kg NK .. + NK - 1 of every column block
+    const uint32_t ts = wv % TS, kg = wv / TS, tok0 = blockIdx.y * TT + 16u * ts;
+    const uint32_t arow = (lane & 15u) * kPfStride + 16u * (lane >> 4);    // A: + 64 ks bytes, + 16 kPfStride i
+    const uint16_t *xrow = p.xt + (uint64_t)min(tok0 + (lane & 15u), p.T - 1u) * f.K16;
+
+    // Every load below is unconditional (clamped addresses, values masked or unused), so the compiler counts them
+    // exactly and each wait covers only what it needs.  Column block cb + 1's streams, raw rows and row-index entry
+    // are requested while cb decodes, and its first activations while cb's last products run.
+    auto coord = [&](uint32_t cb) {
+        Coord0 c = coord0(jj * CB + min(cb, CB - 1u), rg0, f, L);
+        c.rb += 2u * q * f.K16;                                   // this half-wave's first row
+        return c;
+    };
+    auto xload = [&](uint32_t cb, uint32_t i, bf16x8_t &dst) {   // k-step kg NK + i: columns + 8 (lane >> 4) .. + 7
+        cb = min(cb, CB - 1u);
+        const uint32_t col = cb * kCols + 32u * (kg * NK + i) + 8u * (lane >> 4);
+        const uint32_t keep = col < f.K16 ? ~0u : 0u;             // 0 past K16 (its products are skipped or zero)
+        const uint4 v = *(const uint4 *)(xrow + min(col, f.K16 - 8u));
+        dst = __builtin_bit_cast(bf16x8_t, make_uint4(v.x & keep, v.y & keep, v.z & keep, v.w & keep));
+    };
+
+    TabStage<kPeekSeq> Q;
+    Q.issue(a);
+    // column block 0: staged now; column block 1's header byte and base requested
+    Coord0 c = coord(0u);
+    uint4 st0, st1;                                               // column block cb's stream chunks (two per lane)
+    uint32_t start, sh;                                           // lane offset in the block, block offset in the slot
+    bool fits;
+    uint32_t base = a.bases[c.b];
+    pf_stage_issue(a, a.hdr[(uint64_t)c.b * kHdrBytes + L], base, L, lane, st0, st1, start, sh, fits);
+    uint4 raw[2] = {raw_row<ELEM>(a.low, f, c, 0u), raw_row<ELEM>(a.low, f, c, 1u)};
+    uint32_t P0 = part_start(a, c.b, q, L);
+    Coord0 c1 = coord(1u);
+    uint32_t n1 = a.hdr[(uint64_t)c1.b * kHdrBytes + L], base1 = a.bases[c1.b];
+    bf16x8_t xb[AH];
+#pragma unroll
+    for (int d = 0; d < AH; d++) xload((uint32_t)(d / NK), (uint32_t)(d % NK), xb[d]);
+    Q.commit(s);
+    if (copier && fits) pf_stage_commit(slot, lane, st0, st1);
+    Q.finish(s, a);
+    f32x4_t acc[WR];
+#pragma unroll
+    for (int i = 0; i < WR; i++) acc[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    const XRegs<true> xnone{};
+    __syncthreads();                                              // table and column block 0's streams staged
+    for (uint32_t cb = 0; cb < CB; cb++) {
+        // ---- requests for column block cb + 1 (clamped past the last) ----
+        uint4 sn0, sn1;
+        uint32_t startn, shn;
+        bool fitsn;
+        pf_stage_issue(a, n1, base1, L, lane, sn0, sn1, startn, shn, fitsn);
+        uint4 rawn[2] = {raw_row<ELEM>(a.low, f, c1, 0u), raw_row<ELEM>(a.low, f, c1, 1u)};
+        const uint32_t P0n = part_start(a, c1.b, q, L);
+        const Coord0 c2 = coord(cb + 2u);
+        const uint32_t n2 = a.hdr[(uint64_t)c2.b * kHdrBytes + L], base2 = a.bases[c2.b];
+        // ---- decode column block cb into the tile ----
+        uint32_t pw[2][8];
+        if (fits) pf_rows<ELEM>(s, slot + sh + start, P0, raw, xnone, pw);                      // LDS reads
+        else pf_rows<ELEM>(s, (const uint32_t *)(a.data + base) + start, P0, raw, xnone, pw);      // global (rare)
+#pragma unroll
+        for (int r = 0; r < 2; r++) {
+            uint4 *o = (uint4 *)(tile + (8u * j + 2u * q + r) * kPfStride + 32u * L);
+            o[0] = c.col_ok ? make_uint4(pw[r][0], pw[r][1], pw[r][2], pw[r][3]) : make_uint4(0u, 0u, 0u, 0u);
+            o[1] = c.col_ok ? make_uint4(pw[r][4], pw[r][5], pw[r][6], pw[r][7]) : make_uint4(0u, 0u, 0u, 0u);
+        }
+        __syncthreads();                                          // tile complete, slots free
+        if (copier && fitsn) pf_stage_commit(slot, lane, sn0, sn1);   // column block cb + 1's streams
+        // ---- products: this wave's NK k-steps of 32 columns (none past K16 in a last column block under 512) ----
+        const uint32_t kn = min(16u, (f.K16 - cb * kCols + 31u) / 32u);
+        auto wload = [&](int i, bf16x8_t (&dst)[WR]) {
+#pragma unroll
+            for (int r = 0; r < WR; r++)
+                dst[r] = *(const bf16x8_t *)(tile + arow + 16u * kPfStride * r + 64u * (kg * NK + (uint32_t)i));
+        };
+        bf16x8_t wa[2][WR];
+        wload(0, wa[0]);
+#pragma unroll
+        for (int i = 0; i < NK; i++) {
+            if (i + 1 < NK) wload(i + 1, wa[(i + 1) & 1]);
+            if (kg * NK + (uint32_t)i < kn) {
+#pragma unroll
+                for (int r = 0; r < WR; r++)
+                    acc[r] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa[i & 1][r], xb[i % AH], acc[r], 0, 0, 0);
+            }
+            // the ring runs on into the next column block
+            const int nx = i + AH;
+            xload(cb + (uint32_t)(nx / NK), (uint32_t)(nx % NK), xb[i % AH]);
+        }
+        __syncthreads();                                          // tile free, column block cb + 1's streams visible
+        start = startn;
+        sh = shn;
+        fits = fitsn;
+        base = base1;
+        raw[0] = rawn[0];
+        raw[1] = rawn[1];
+        P0 = P0n;
+        c = c1;
+        c1 = c2;
+        n1 = n2;
+        base1 = base2;
+    }
+    // ---- the KS waves of a token group add their partial sums through LDS (the tile is free after the last barrier) ----
+    if constexpr (KS > 1) {
+        float *red = (float *)tile;                                // [wave][row subtile][4][64 lanes]
+#pragma unroll
+        for (int r = 0; r < WR; r++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) red[((wv * WR + r) * 4 + e) * 64u + lane] = acc[r][e];
+        __syncthreads();
+        if (kg != 0) return;
+#pragma unroll
+        for (uint32_t g = 1; g < (uint32_t)KS; g++)
+#pragma unroll
+            for (int r = 0; r < WR; r++)
+#pragma unroll
+                for (int e = 0; e < 4; e++) acc[r][e] += red[(((g * TS + ts) * WR + r) * 4 + e) * 64u + lane];
+    }
+    // ---- y: lane holds rows 4 (lane >> 4) + e of each 16-row subtile, for token lane & 15 ----
+    uint16_t *y = (uint16_t *)a.out;
+    const uint32_t t = tok0 + (lane & 15u);
+    if (t >= p.T) return;
+#pragma unroll
+    for (int r = 0; r < WR; r++) {
+        const uint32_t m = rg0 * kRows0 + 16u * r + 4u * (lane >> 4);
+        uint32_t h[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const uint32_t me = min(m + (uint32_t)e, a.M - 1u);
+            float v = acc[r][e];
+            if (a.scale) v *= a.scale[me];
+            if (a.bias) v += __uint_as_float((uint32_t)a.bias[me] << 16);
+            h[e] = f32_to_bf16_rne(v);
+        }
+        uint16_t *o = y + (uint64_t)t * a.M + m;
+        if ((a.M & 3u) == 0u && m + 3u < a.M) {
+            *(uint2 *)o = make_uint2(h[0] | h[1] << 16, h[2] | h[3] << 16);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                if (m + (uint32_t)e < a.M) o[e] = (uint16_t)h[e];
+        }
+    }
+}
+
+int launch_prefill0(int elem_t, uint32_t tt, const PrefillArgs &p, hipStream_t st) {
+    const Shape f(p.a.M, p.a.K, 0);
+    const dim3 grid((f.groups() + kPfRows / kRows0 - 1u) / (kPfRows / kRows0), (p.T + tt - 1u) / tt), block(1024);
+    const size_t lds = (size_t)kPfRows * kPfStride + 8u * kPfSlot * 4u;
+#define NWC_PF(E, T_) hipLaunchKernelGGL((k_prefill0<E, T_>), grid, block, lds, st, p)
+    if (elem_t == kElemFp8) {
+        switch (tt) { case 64: NWC_PF(kElemFp8, 64); break; case 128: NWC_PF(kElemFp8, 128); break;
+                      default: NWC_PF(kElemFp8, 256); break; }
+    } else {
+        switch (tt) { case 64: NWC_PF(kElemBf16, 64); break; case 128: NWC_PF(kElemBf16, 128); break;
+                      default: NWC_PF(kElemBf16, 256); break; }
+    }
+#undef NWC_PF
+    return (int)hipGetLastError();
+}
+
 }  // namespace nwc

@@ -456,6 +456,14 @@ struct BlockArgs {
     const uint32_t *seq;    // 13-bit token-path decode table (nwc_seq_table) or null
 };
 
+// Prefill without a temporary BF16 matrix (k_prefill0): the matrix in `a` (a.out = y [T x M] BF16, a.aux = row index,
+// a.seq = 13-bit table, both required), activations [T x K16] BF16.
+struct PrefillArgs {
+    BlockArgs a;
+    const uint16_t *xt;
+    uint32_t T;
+};
+
 struct GatherArgs {
     const uint8_t *data;
     const uint32_t *bases;

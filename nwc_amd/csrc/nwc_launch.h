@@ -20,6 +20,8 @@ int launch_gather_prefix(int layout, int elem_t, const GatherArgs &a, hipStream_
 // layout-0 token path for ntok (2..4) activation vectors at once (k_layout0_batch); plan from plan_layout0_batch
 int launch_layout0_batch(const LaunchPlan &p, int elem_t, const BlockArgs &a, uint32_t ntok, hipStream_t st);
 int launch_gather_fixed(int elem_t, const GatherArgs &a, hipStream_t st);
+// layout-0 prefill (k_prefill0): tt tokens per workgroup tile (64, 128, 256 or 512)
+int launch_prefill0(int elem_t, uint32_t tt, const PrefillArgs &p, hipStream_t st);
 int launch_ref_fp8(const uint8_t *w, const float *scale, const float *x, uint16_t *y, uint32_t M, uint32_t K, int ncu,
                    hipStream_t st);
 

@@ -43,6 +43,10 @@ ROW_INDEX = os.environ.get("NWC_ROW_INDEX", "1") != "0"   # layouts 0/1: build t
 # temporary BF16 matrix + F.linear
 BATCH_MAX = int(os.environ.get("NWC_BATCH_MAX", "8"))
 BATCH_LAUNCH = 4                                           # vectors per nwc_linear_xbf16_batch launch
+# more tokens, layout 0: "dequant" (default) decompresses into a temporary BF16 matrix and calls F.linear (hipBLASLt);
+# "fused" runs nwc_prefill_xbf16 (decode into LDS + matrix cores, no temporary matrix; correct, but slower on MI355X
+# at 512 tokens: 20 ms against 8.5 ms per Qwen3-4B stack)
+PREFILL = os.environ.get("NWC_PREFILL", "dequant")
 FP8_MAX = 448.0
 
 
@@ -362,6 +366,24 @@ class NWCWeight:
                  ptr(self.scale), ptr(y[t0]), self.n, self.in_features, self.code, nt)
         return y
 
+    def prefill(self, x: torch.Tensor, bias) -> torch.Tensor:
+        """Several BF16 tokens at once, layout 0, without a temporary BF16 matrix: x [T, in_features] -> y BF16
+        [T, out_features] = x W^T (fp8: times the row scales) + bias, accumulated in fp32 on the matrix cores
+        (nwc_prefill_xbf16; equal to F.linear on the decompressed matrix up to fp32 summation order)."""
+        _need_gpu(self.data)
+        if self.layout != 0:
+            raise ValueError("prefill: layout 0 only")
+        T = x.shape[0]
+        if self.K16 == self.in_features and x.dtype == torch.bfloat16 and x.is_contiguous():
+            xin = x
+        else:
+            xin = torch.zeros(T, self.K16, dtype=torch.bfloat16, device=x.device)
+            xin[:, :self.in_features] = x
+        y = torch.empty(T, self.out_features, dtype=torch.bfloat16, device=x.device)
+        call("nwc_prefill_xbf16", stream(), *self._streams(), ptr(self.row_index()), ptr(self.seq_table()), ptr(xin),
+             ptr(bias), ptr(self.scale), ptr(y), self.n, self.in_features, self.code, T)
+        return y
+
     def gather(self, ids: torch.Tensor) -> torch.Tensor:
         """Rows `ids` as BF16 [..., in_features], decoded straight from the compressed matrix (embedding lookup)."""
         _need_gpu(self.data)
@@ -406,7 +428,8 @@ def _bf16_bias(bias, device):
 class NWCLinear(nn.Module):
     """nn.Linear over a compressed matrix (elem "bf16" lossless, or "fp8" weight-only).  One BF16 token goes through
     the fused decode-matvec kernel, up to NWC_BATCH_MAX (8) BF16 tokens of a layout-0 matrix through the batched one
-    (the matrix decoded once per four tokens); anything else through a temporary BF16 matrix and F.linear."""
+    (the matrix decoded once per four tokens); anything else through a temporary BF16 matrix and F.linear, or, with
+    NWC_PREFILL=fused, BF16 tokens of a layout-0 matrix through the fused prefill kernel (NWCWeight.prefill)."""
 
     def __init__(self, linear: nn.Linear = None, device="cuda", block=None, w: "NWCWeight" = None, bias=None,
                  elem="bf16"):
@@ -427,6 +450,10 @@ class NWCLinear(nn.Module):
         tokens = x.numel() // self.in_features
         if x.dtype == torch.bfloat16 and self.w.layout == 0 and 1 < tokens <= BATCH_MAX and self.w.K16 <= 16384:
             y = self.w.linear_batch(x.reshape(tokens, self.in_features), self._bias_data())
+            return y.view(*x.shape[:-1], self.out_features)
+        if (PREFILL == "fused" and x.dtype == torch.bfloat16 and self.w.layout == 0 and self.w.row_index() is not None
+                and self.w.seq_table() is not None):
+            y = self.w.prefill(x.reshape(tokens, self.in_features), self._bias_data())
             return y.view(*x.shape[:-1], self.out_features)
         weight = self.w.dequant()
         if self.w.scale is None:

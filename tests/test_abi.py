@@ -29,7 +29,7 @@ def test_header_declares_the_reference_exports():
     d = _declared()
     assert REFERENCE_EXPORTS <= d
     assert d - REFERENCE_EXPORTS == {"nwc_linear_xbf16", "nwc_linear_xbf16_batch", "nwc_row_index", "nwc_token_split",
-                                     "nwc_seq_table", "nwc_dequant_seq"}                                 # this build's additions
+                                     "nwc_seq_table", "nwc_dequant_seq", "nwc_prefill_xbf16"}           # this build's additions
 
 
 def test_library_exports_every_declared_symbol():
@@ -93,6 +93,8 @@ def _device_entry(lib):
     lib.nwc_linear_xbf16.argtypes = [P, P, P, P, P, P, P, P, P, P, P, P, U64, U32, I]
     lib.nwc_linear_xbf16_batch.restype = I
     lib.nwc_linear_xbf16_batch.argtypes = [P, P, P, P, P, P, P, P, P, P, P, U64, U32, I, U32]
+    lib.nwc_prefill_xbf16.restype = I
+    lib.nwc_prefill_xbf16.argtypes = [P, P, P, P, P, P, P, P, P, P, P, P, U64, U32, I, U32]
     return lib
 
 
@@ -101,6 +103,22 @@ def test_batch_entry_point_refusals(elem, ntok):
     """nwc_linear_xbf16_batch takes layout 0 and 1..4 vectors; anything else gets -1 before any device call."""
     lib = _device_entry(_lib())
     assert lib.nwc_linear_xbf16_batch(None, *([None] * 10), 2560 * 4096, 4096, elem, ntok) == -1
+
+
+@pytest.mark.parametrize("elem,index,table,ntok,want", [
+    (0x10, 1, 1, 512, -1),      # layout 1
+    (0x20, 1, 1, 512, -1),      # layout 2
+    (0x00, 0, 1, 512, -1),      # no row index
+    (0x00, 1, 0, 512, -1),      # no 13-bit table
+    (0x00, 1, 1, 0, 0),         # no tokens: nothing to do
+    (0x01, 1, 1, 65535 * 64 + 1, -1),
+])
+def test_prefill_entry_point_refusals(elem, index, table, ntok, want):
+    """nwc_prefill_xbf16 answers these before any device call (dummy non-null pointers are never dereferenced)."""
+    lib = _device_entry(_lib())
+    dummy = ctypes.c_void_p(8)
+    args = [None] * 6 + [dummy if index else None, dummy if table else None] + [None] * 4
+    assert lib.nwc_prefill_xbf16(*args, 2560 * 4096, 4096, elem, ntok) == want
 
 
 @pytest.mark.parametrize("M,K,elem,ok", [
@@ -131,3 +149,4 @@ def test_device_entry_points_refuse_unaddressable_planes(M, K, elem, ok):
     assert lib.nwc_matvec(None, *([None] * 7), n, 4096, K, elem) == -1
     assert lib.nwc_linear_xbf16(None, *([None] * 11), n, K, elem) == -1
     assert lib.nwc_linear_xbf16_batch(None, *([None] * 10), n, K, elem, 2) == -1
+    assert lib.nwc_prefill_xbf16(None, *([None] * 11), n, K, elem, 512) == -1
