@@ -198,22 +198,67 @@ __device__ __forceinline__ float row0(Seq<ELEM, STRIDE> &S, const Tab &s, const 
 }
 
 // Raw rows in flight per half-wave: two.  The prologue requests rows 0-1 only once the wave's stream chunks have
-// arrived, so decoding starts sooner; each later row has one row's decode time to arrive (a deeper ring, or rows
-// requested together with the streams, measured slower: the whole chip's first requests compete for HBM, and the
-// workgroup waits for all of its streams).
+// arrived, so decoding starts sooner (a deeper ring, or rows requested together with the streams, measured slower:
+// the whole chip's first requests compete for HBM, and the workgroup waits for all of its streams).
 constexpr int kRing0 = 2;
 
+// The table entries of one row's 16 weights for one lane (four steps of the cursor; a step that was not fast in some
+// lane is redone code by code by the whole wave), kept apart from their use so that a row can be decoded before its
+// raw bytes have arrived.
+template <int ELEM, class Tab>
+__device__ __forceinline__ void row_codes(Seq<ELEM> &S, const Tab &s, uint32_t (&e1)[4], uint32_t (&e2)[4]) {
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const uint32_t s0 = S.s;
+        const uint32_t *wp0 = S.wp;
+        if (__any(S.fast_quad(s, e1[k], e2[k]) >= kSeqSlowTest)) {
+            S.s = s0;
+            S.wp = wp0;
+            S.reload();
+            S.slow_quad(s, e1[k], e2[k]);
+        }
+    }
+}
+// The lane's partial dot product of one row from its entries, raw bytes and activations (token and fp32 modes).
+template <int MODE, bool XBF16>
+__device__ __forceinline__ float row_dot(const uint32_t (&e1)[4], const uint32_t (&e2)[4], const uint4 &rw,
+                                         const XRegs<XBF16> &x) {
+    float sum = 0.f;
+    uint32_t pw[8];
+#pragma unroll
+    for (int k = 0; k < 4; k++) use_quad<MODE, XBF16>(e1[k], e2[k], u4_get(rw, k), k, x, sum, pw);
+    asm volatile("" : "+v"(sum));                            // one row's products before the next row's
+    return sum;
+}
+
 // Rows r0 .. r0 + NR - 1 of one layout-0 block for one lane, decoded from LDS starting at bit position P0 of the
-// lane's stream, with the first kRing0 of those raw-plane rows already requested into `ring` (c.rb is row r0's offset).  Returns the row sums
-// reduced over the half-wave (NR = 8: lane 4r holds row r0 + r; NR = 4: lane 8r) or, for dequantization, stores the
-// rows; MODE kRowIndex records the row index (positions of rows 2, 4, 6) instead.  Fully unrolled: every row's raw
-// bytes live in their own registers.
+// lane's stream, with the first kRing0 of those raw-plane rows already requested into `ring` (c.rb is row r0's
+// offset).  Returns the row sums reduced over the half-wave (NR = 8: lane 4r holds row r0 + r; NR = 4: lane 8r) or,
+// for dequantization, stores the rows; MODE kRowIndex records the row index (positions of rows 2, 4, 6) instead.
+// Fully unrolled: every row's raw bytes live in their own registers.
+// The row sums are formed one row behind the decode: row r's table entries wait while row r + 1 is decoded, so a
+// wave decodes its first two rows before it needs its first raw row, and each later raw row has two rows' decode
+// time to arrive (Qwen3-4B sweep 1726 -> 1695 us per token; two rows behind measured slower, 1743 us).
 template <int ELEM, int MODE, bool XBF16, int NR, class Tab>
 __device__ __forceinline__ float rowsN(const Tab &s, const uint32_t *lane, uint32_t P0, const BlockArgs &a, const Shape &f,
                                        const XRegs<XBF16> &x, uint4 ring[kRing0], const Coord0 &c, uint32_t r0, uint32_t L) {
     Seq<ELEM> S;
     S.init_at(lane, P0);
     float acc[NR];
+    if constexpr (MODE == kToken || MODE == kF32) {
+        uint32_t e1[2][4], e2[2][4];                          // entries of rows r (slot r & 1) and r + 1
+        row_codes(S, s, e1[0], e2[0]);
+#pragma unroll
+        for (int r = 0; r < NR; r++) {
+            if (r + 1 < NR) row_codes(S, s, e1[(r + 1) & 1], e2[(r + 1) & 1]);
+            const float sum = row_dot<MODE, XBF16>(e1[r & 1], e2[r & 1], ring[r % kRing0], x);
+            if (r + kRing0 < NR) ring[r % kRing0] = raw_row<ELEM>(a.low, f, c, r + kRing0);
+            acc[r] = c.col_ok ? sum : 0.f;
+        }
+        if constexpr (NR == 8) return reduce8_transposed(acc, L);
+        else if constexpr (NR == 4) return reduce4_transposed(acc, L);
+        else return reduce2_transposed(acc, L);
+    }
 #pragma unroll
     for (int r = 0; r < NR; r++) {
         if (MODE == kRowIndex && r > 0 && (r & 1) == 0)
