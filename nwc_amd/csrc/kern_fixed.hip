@@ -103,6 +103,7 @@ __global__ void __launch_bounds__(1024) k_layout2(BlockArgs a) {
     const uint8_t *rplane = a.low + f.nib2_bytes();
     const uint32_t rg0 = blockIdx.x * a.G;
     const uint32_t ng = min(a.G, f.groups() - rg0);
+    const RowFinish fin = row_finish_load<MODE, ELEM == kElemFp8>(a, rg0 * kRows12, ng * kRows12);
     const uint32_t nt = ng * f.CB;
 
     for (uint32_t t = hw; t < nt; t += nhw) {
@@ -198,7 +199,7 @@ __global__ void __launch_bounds__(1024) k_layout2(BlockArgs a) {
             }
         }
     }
-    if (MODE != kDequant) finish_rows<MODE>(a, part, rg0 * kRows12, ng * kRows12, f.CB);
+    if (MODE != kDequant) finish_rows<MODE>(a, part, rg0 * kRows12, ng * kRows12, f.CB, ELEM == kElemFp8 ? &fin : nullptr);
 }
 
 // BF16 token path: a workgroup owns G whole 16-row groups; each half-wave decodes super-chunks sc0 .. sc0 + NS - 1

@@ -410,6 +410,7 @@ __global__ void __launch_bounds__(1024) k_layout0(BlockArgs a) {
     // and activations; loads complete in order, so each wait below covers only what it needs
     uint32_t t = hw / SP;
     const uint32_t r0 = (hw % SP) * NR;                       // first row of this half-wave's share of the block
+    const RowFinish fin = row_finish_load<MODE>(a, rg0 * kRows0, ng * kRows0);
     Coord0 c = coord0(min(t, tl), rg0, f, L);
     Region R = region_of(a, B0, B0 + min(HB, nt), nb, mend);
     if constexpr (!PIPE) {
@@ -429,18 +430,20 @@ __global__ void __launch_bounds__(1024) k_layout0(BlockArgs a) {
     if (ROWS) load_x16<XBF16>(x, a.x, c.col0, c.col_ok);
 
     if constexpr (!PIPE) {
-        // everything but the raw rows is requested before the first wait; rows 0-1 once this wave's stream chunks
-        // are in (requested together with the streams they delay them: o_proj 8.1 -> 8.7 us, qkv 9.1 -> 9.6)
+        // everything but the raw rows is requested before the first wait; rows 0-1 once the workgroup's streams are
+        // in, since the first raw row is needed only after two rows' decode (requested together with the streams
+        // they delay them: o_proj 8.1 -> 8.7 us, qkv 9.1 -> 9.6; after this wave's own chunks, before the barrier:
+        // 4B sweep 0.2% slower)
         const uint32_t P0 = NR == 8 ? 0u : part_start(a, c.b, r0 >> 1, L);
         Q.commit(s);
         Q.finish(s, a);
         const bool fits = R.n16 * 4u <= cap;
         if (fits) bulk_commit(Bk, cur, R, tid, nth);
         uint4 raw[kRing0];
+        __syncthreads();
 #pragma unroll
         for (int r = 0; r < (NR < kRing0 ? NR : kRing0); r++)
             raw[r] = MODE == kRowIndex ? make_uint4(0u, 0u, 0u, 0u) : raw_row<ELEM>(a.low, f, c, r);
-        __syncthreads();
         if (t < nt) {
             const uint32_t start = c.col_ok ? half_scan_incl(n, L) - n : 0u;
             float v;
@@ -499,7 +502,7 @@ __global__ void __launch_bounds__(1024) k_layout0(BlockArgs a) {
             t += H;
         }
     }
-    if (ROWS) finish_rows<MODE>(a, part, rg0 * kRows0, ng * kRows0, f.CB);
+    if (ROWS) finish_rows<MODE>(a, part, rg0 * kRows0, ng * kRows0, f.CB, &fin);
 }
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -577,6 +580,7 @@ __global__ void __launch_bounds__(1024) k_layout1(BlockArgs a) {
     const Shape f(a.M, a.K, 1);
     const uint32_t rg0 = blockIdx.x * a.G;
     const uint32_t ng = min(a.G, f.groups() - rg0);
+    const RowFinish fin = row_finish_load<MODE, ELEM == kElemFp8>(a, rg0 * kRows12, ng * kRows12);
     const uint32_t nt = ng * f.CB;
 
     for (uint32_t t = hw; t < nt; t += nhw) {
@@ -598,7 +602,7 @@ __global__ void __launch_bounds__(1024) k_layout1(BlockArgs a) {
             part[(g * kRows12 + r + 8) * f.CB + cb] = v.y;
         }
     }
-    if (MODE != kDequant) finish_rows<MODE>(a, part, rg0 * kRows12, ng * kRows12, f.CB);
+    if (MODE != kDequant) finish_rows<MODE>(a, part, rg0 * kRows12, ng * kRows12, f.CB, ELEM == kElemFp8 ? &fin : nullptr);
 }
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -802,6 +806,7 @@ __global__ void __launch_bounds__(1024) k_layout1s(BlockArgs a) {
     float *part = (float *)(xs + (ROWS ? n8 : 0u));
     const uint32_t rg0 = blockIdx.x * a.G;
     const uint32_t ng = min(a.G, f.groups() - rg0);
+    const RowFinish fin = row_finish_load<MODE, ELEM == kElemFp8>(a, rg0 * kRows12, ng * kRows12);
     const uint32_t nt = ng * f.CB, tl = nt - 1u;
     const uint32_t B0 = rg0 * f.CB, nb = f.nb;
     const uint32_t mend = B0 + nt == nb ? matrix_end(a, nb) : 0u;
@@ -850,7 +855,7 @@ __global__ void __launch_bounds__(1024) k_layout1s(BlockArgs a) {
             part[pi + 8u * f.CB * SP] = v.y;                   // row r + 8
         }
     }
-    if (ROWS) finish_rows<MODE>(a, part, rg0 * kRows12, ng * kRows12, f.CB * SP);
+    if (ROWS) finish_rows<MODE>(a, part, rg0 * kRows12, ng * kRows12, f.CB * SP, ELEM == kElemFp8 ? &fin : nullptr);
 }
 
 // Layout 1, several items per half-wave: for matrices whose row groups hold more blocks than a workgroup has
@@ -869,6 +874,7 @@ __global__ void __launch_bounds__(1024) k_layout1m(BlockArgs a) {
     const Shape f(a.M, a.K, 1);
     const uint32_t rg0 = blockIdx.x * a.G;
     const uint32_t ng = min(a.G, f.groups() - rg0);
+    const RowFinish fin = row_finish_load<MODE, ELEM == kElemFp8>(a, rg0 * kRows12, ng * kRows12);
     const uint32_t nt = ng * f.CB;
     const uint32_t cap = a.slot_words * a.G * f.CB;
     const uint32_t n8 = (f.K16 + 31u) / 32u * 4u;
@@ -943,7 +949,7 @@ __global__ void __launch_bounds__(1024) k_layout1m(BlockArgs a) {
         base = basen;
         P0 = P0n;
     }
-    finish_rows<MODE>(a, part, rg0 * kRows12, ng * kRows12, f.CB * SP);
+    finish_rows<MODE>(a, part, rg0 * kRows12, ng * kRows12, f.CB * SP, ELEM == kElemFp8 ? &fin : nullptr);
 }
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -1227,6 +1233,13 @@ __global__ void __launch_bounds__(1024) k_layout0_batch(BlockArgs a) {
     const uint32_t B0 = rg0 * f.CB, nb = f.nb;
     const uint32_t mend = B0 + nt == nb ? matrix_end(a, nb) : 0u;
     const uint32_t t = hw;
+    // fp8: the scale and bias of this thread's first output (row rg0 * 8 + tid / NT), requested first (as
+    // row_finish_load does)
+    float fin_scale = 1.f, fin_bias = 0.f;
+    if (ELEM == kElemFp8 && tid < ng * kRows0 * NT && rg0 * kRows0 + tid / NT < a.M) {
+        if (a.scale) fin_scale = a.scale[rg0 * kRows0 + tid / NT];
+        if (a.bias) fin_bias = __uint_as_float((uint32_t)a.bias[rg0 * kRows0 + tid / NT] << 16);
+    }
     const Coord0 c = coord0(min(t, tl), rg0, f, L);
     const Region R = region_of(a, B0, B0 + min(H, nt), nb, mend);
     TabStage<PEEK> Q;
@@ -1261,8 +1274,9 @@ __global__ void __launch_bounds__(1024) k_layout0_batch(BlockArgs a) {
         if (row >= a.M) continue;
         float acc = 0.f;
         for (uint32_t cb = 0; cb < f.CB; cb++) acc += part[(rr * f.CB + cb) * NT + u];
-        if (a.scale) acc *= a.scale[row];
-        if (a.bias) acc += __uint_as_float((uint32_t)a.bias[row] << 16);
+        const bool first = ELEM == kElemFp8 && i == threadIdx.x;
+        if (a.scale) acc *= first ? fin_scale : a.scale[row];
+        if (a.bias) acc += first ? fin_bias : __uint_as_float((uint32_t)a.bias[row] << 16);
         ((uint16_t *)a.out)[(uint64_t)u * a.M + row] = (uint16_t)f32_to_bf16_rne(acc);
     }
 }

@@ -484,10 +484,30 @@ enum Mode { kToken = 0, kDequant = 1, kF32 = 2, kRowIndex = 3 };
 // several half-waves decode one block's rows in parallel.
 constexpr uint32_t kRowIndexSplits = 3;
 
+// The scale and bias of the first row a thread finishes (row0 + threadIdx.x), requested before the kernel's other
+// loads so that the finish does not wait a memory round trip for them (and so that no later wait covers them).
+// PRE = false loads nothing (kernels that keep the finish's own loads where a matrix rarely has either: the held
+// registers and the branch cost more there than the round trip).
+struct RowFinish {
+    float scale, bias;
+};
+template <int MODE, bool PRE = true>
+__device__ __forceinline__ RowFinish row_finish_load(const BlockArgs &a, uint32_t row0, uint32_t nrows) {
+    RowFinish r{1.f, 0.f};
+    const uint32_t row = row0 + threadIdx.x;
+    if (PRE && MODE == kToken && threadIdx.x < nrows && row < a.M) {
+        if (a.scale) r.scale = a.scale[row];
+        if (a.bias) r.bias = __uint_as_float((uint32_t)a.bias[row] << 16);
+    }
+    return r;
+}
+
 // Workgroup epilogue of the token / fp32 paths: rows of the tile summed over the column blocks (ascending),
-// times scale, plus bias, rounded to BF16 (token) or written as fp32.
+// times scale, plus bias, rounded to BF16 (token) or written as fp32.  `pre`: this thread's first row's scale and
+// bias, already loaded.
 template <int MODE>
-__device__ __forceinline__ void finish_rows(const BlockArgs &a, const float *part, uint32_t row0, uint32_t nrows, uint32_t CB) {
+__device__ __forceinline__ void finish_rows(const BlockArgs &a, const float *part, uint32_t row0, uint32_t nrows, uint32_t CB,
+                                            const RowFinish *pre = nullptr) {
     __syncthreads();
     for (uint32_t i = threadIdx.x; i < nrows; i += blockDim.x) {
         const uint32_t row = row0 + i;
@@ -495,8 +515,9 @@ __device__ __forceinline__ void finish_rows(const BlockArgs &a, const float *par
         float v = 0.f;
         for (uint32_t cb = 0; cb < CB; cb++) v += part[i * CB + cb];
         if (MODE == kToken) {
-            if (a.scale) v *= a.scale[row];
-            if (a.bias) v += __uint_as_float((uint32_t)a.bias[row] << 16);
+            const bool first = pre && i == threadIdx.x;
+            if (a.scale) v *= first ? pre->scale : a.scale[row];
+            if (a.bias) v += first ? pre->bias : __uint_as_float((uint32_t)a.bias[row] << 16);
             ((uint16_t *)a.out)[row] = (uint16_t)f32_to_bf16_rne(v);
         } else {
             ((float *)a.out)[row] = v;
