@@ -100,13 +100,13 @@ bool plan_layout0_tiers(const Shape &f, int mode, int ncu, bool index, uint32_t 
     // 1. with the row index, four or two half-waves per block (rows 0-1 / 2-3 / 4-5 / 6-7 or rows 0-3 / 4-7), up to
     //    32 half-waves (16 waves) per workgroup; two per block only up to 20 half-waves when two workgroups share a CU;
     // 2. else one half-wave per block, up to 32 blocks (the 58-VGPR kernel allows 8 waves per SIMD).
-    auto one_round = [&](uint32_t wgpc) {
+    auto one_round = [&](uint32_t wgpc, uint32_t split2_max) {
         const uint32_t G = std::max(1u, ceil_div(groups, wgpc * ncu_)), blocks = G * CB;
         if (index && (rows || mode == kDequant)) {
             const uint32_t lds = blocks * kSlotWords0 * 4u + G * part;
             if (lds <= budget) {
                 if (4u * blocks <= 32u) return set(false, 4u, G, 4u * blocks, kSlotWords0, lds);
-                if (2u * blocks <= (wgpc == 1u ? 32u : 20u)) return set(false, 2u, G, 2u * blocks, kSlotWords0, lds);
+                if (2u * blocks <= split2_max) return set(false, 2u, G, 2u * blocks, kSlotWords0, lds);
             }
         }
         const uint32_t halves = (blocks + 1u) & ~1u;
@@ -121,7 +121,11 @@ bool plan_layout0_tiers(const Shape &f, int mode, int ncu, bool index, uint32_t 
     // 4096x1024 and gate_up 6144x1024 11-12% faster.  Otherwise, or when that tile does not fit, two per CU.
     const uint32_t G2 = std::max(1u, ceil_div(groups, 2u * ncu_)), G1 = ceil_div(groups, ncu_);
     const uint32_t load2 = G2 * ceil_div(ceil_div(groups, G2), ncu_);
-    if (stage == kOneRound) return ((G2 * CB <= 4u || G1 <= load2) && one_round(1u)) || one_round(2u);
+    // With the row index, a token tile too large to split over two half-waves per block at one workgroup per CU (more
+    // than 16 blocks) loses to the two-per-CU tile that can (up to 32 half-waves): 9728x2560 (1216 groups) 256 x
+    // (5 groups, 26 half-waves) 11.0-11.3 us -> 406 x (3, 30) 10.9-11.0 us.
+    if (stage == kOneRound && index && rows && 2u * G1 * CB > 32u && 2u * G2 * CB <= 32u && one_round(2u, 32u)) return true;
+    if (stage == kOneRound) return ((G2 * CB <= 4u || G1 <= load2) && one_round(1u, 32u)) || one_round(2u, 20u);
     // 2m. one block per half-wave over several residency rounds, when one round's tile would exceed 32 blocks: the
     //     largest tile of at most 32 blocks whose LDS fits the budget (24 blocks next to the 13-bit table, 32 next to
     //     the 12-bit one).  The rounds overlap one workgroup's stream copy with another's decode, which the pipelined
