@@ -240,6 +240,7 @@ def test_row_index_values(cuda, M, K, escapes):
     (0, 2560, 4096, 2, "none"), (0, 6144, 2560, 2, "none"), (0, 1003, 1100, 4, "none"), (0, 2560, 4096, 2, "sparse"),
     (0, 2560, 4096, 2, "dense"), (0, 6144, 2560, 2, "dense"), (0, 1003, 1100, 4, "dense"), (0, 2560, 4096, 2, "heavy"),
     (0, 6144, 2560, 2, "heavy"), (0, 19456, 2560, 1, "heavy"), (0, 2560, 9728, 1, "dense"), (0, 151936, 256, 1, "none"),
+    (0, 9728, 2560, 2, "none"), (0, 9728, 2560, 2, "heavy"),  # two per CU, two half-waves per block on 30 half-waves
     (1, 2560, 4096, 4, "none"), (1, 6144, 2560, 4, "none"), (1, 19456, 2560, 2, "none"), (1, 1003, 1100, 4, "none"),
     (1, 2560, 4096, 4, "dense"), (1, 1003, 1100, 4, "dense"),
     (1, 2560, 9728, 4, "none"), (1, 2560, 9728, 4, "dense"), (1, 1003, 9000, 4, "none"), (1, 2560, 4096, 4, "heavy"),
