@@ -144,7 +144,8 @@ def test_config2_tied_lm_head(cuda):
 @pytest.mark.parametrize("layout", [0, 1])
 @pytest.mark.parametrize("name", ["gate_up", "down"])
 def test_config3_fp8_large(cuda, name, layout):
-    """weight-only fp8 at the 4B gate_up and down shapes: codes bit-exact, token and fp32 paths."""
+    """weight-only fp8 at the 4B gate_up and down shapes: codes bit-exact, token (with and without a bias)
+    and fp32 paths."""
     NWCWeight, _, quantize_fp8 = _nwc()
     M, K = QWEN3_4B[name]
     print(f"configs[3] fp8 {name} {M}x{K} layout {layout}", flush=True)
@@ -159,6 +160,8 @@ def test_config3_fp8_large(cuda, name, layout):
     y64 = y_exact(d, x.float(), scale=scale)
     check_token(c.linear_bf16(x.cuda(), None), y64)
     check_f32(c.matvec(x.float().cuda()), y64)
+    bias = (torch.rand(M, generator=torch.Generator().manual_seed(K)) - 0.5).to(torch.bfloat16)
+    check_token(c.linear_bf16(x.cuda(), bias.cuda()), y_exact(d, x.float(), scale=scale, bias=bias.float()))
 
 
 @pytest.mark.parametrize("layout", [0, 1, 2])
