@@ -4,8 +4,8 @@ HBM GB/s, Qwen3-4B shapes, batch 1, vs a BF16 hipBLASLt matvec).
 
 Default workload: a Qwen3-4B-shaped stack of 36 layers, each with the fused qkv 6144x2560,
 o_proj 2560x4096, fused gate_up 19456x2560 and down 2560x9728 matrices, BF16, layout 0 (--layout 1 for the other
-layout of that config).  One step = one token: the 144 token-path matvecs of the stack, captured once as a HIP graph
-and replayed.  Weights are N(0, 0.02^2) from fixed seeds; each of the four matrices is encoded once and copied to
+layout of that config; --layout 2 for the fixed-width format on the same stack, outside BASELINE's configs).  One
+step = one token: the 144 token-path matvecs of the stack, captured once as a HIP graph and replayed.  Weights are N(0, 0.02^2) from fixed seeds; each of the four matrices is encoded once and copied to
 36 distinct device buffers (the sweep reads 36 x 4 different buffers, far beyond the 256 MB Infinity Cache).
 
 Reported: value = algorithmic bytes per token / GPU time per token (GB/s), with per-launch times (a HIP graph of the
@@ -937,7 +937,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--layout", type=int, default=0, choices=[0, 1])
+    ap.add_argument("--layout", type=int, default=0, choices=[0, 1, 2])
     ap.add_argument("--runs", type=int, default=60, help="launches per shape for the per-launch medians")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
