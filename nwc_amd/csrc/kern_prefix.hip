@@ -820,7 +820,8 @@ __global__ void __launch_bounds__(1024) k_layout1s(BlockArgs a) {
     bulk_issue(Bk, a.data, R, tid, nth);
     XStage<XBF16> X;
     if (ROWS) x_issue<XBF16>(X, a.x, n8, tid, nth);
-    // as in k_layout0: the raw chunks are requested once this wave's stream chunks are in
+    // the raw chunks are requested once this wave's stream chunks are in, before the barrier (the first one is used
+    // by the first decode step)
     const uint32_t P0 = SP == 1 ? 0u : part_start(a, c.b, sc0 / 4u, L);
     Q.commit(s);
     if (ROWS) {
