@@ -98,7 +98,8 @@ bool plan_layout0_tiers(const Shape &f, int mode, int ncu, bool index, uint32_t 
     };
     // One residency round, wgpc workgroups per CU of G = ceil(groups / (wgpc CUs)) row groups each:
     // 1. with the row index, four or two half-waves per block (rows 0-1 / 2-3 / 4-5 / 6-7 or rows 0-3 / 4-7), up to
-    //    32 half-waves (16 waves) per workgroup; two per block only up to 20 half-waves when two workgroups share a CU;
+    //    32 half-waves (16 waves) per workgroup; two per block only up to 20 half-waves when two workgroups share a CU
+    //    (up to 32 in the exception below);
     // 2. else one half-wave per block, up to 32 blocks (the 58-VGPR kernel allows 8 waves per SIMD).
     auto one_round = [&](uint32_t wgpc, uint32_t split2_max) {
         const uint32_t G = std::max(1u, ceil_div(groups, wgpc * ncu_)), blocks = G * CB;
