@@ -752,6 +752,20 @@ def run_gather(args):
         us = timed_steps(g.replay if g is not None else (lambda: [c.gather(i) for i in ids]), 5, 2) / 16 * 1e3
         out[f"layout{layout}"] = {"us": round(us, 2), "table_MB": round(c.bytes / 1e6, 1),
                                   "out_KB": round(n * K * 2 / 1e3, 1)}
+        if layout <= 1:
+            # NWCWeight.gather takes nwc_gather_xindex (row index) here; the reference's entry point for comparison
+            from nwc_amd._abi import lib as _lib, ptr as _ptr, stream as _stream
+            rows = torch.empty(n, c.K16, dtype=torch.bfloat16, device=dev)
+            ref = lambda j: _lib.nwc_gather(_stream(), *c._streams(), _ptr(ids[j]), n, _ptr(rows), c.n, c.block, K, c.code)
+            ref(0)
+            if not torch.equal(rows[:, :K].cpu(), w[ids[0].cpu()]):
+                raise SystemExit(f"layout {layout}: nwc_gather is not bit-exact")
+            g2 = graph_stack([(lambda j=j: ref(j)) for j in range(16)])
+            us2 = timed_steps(g2.replay if g2 is not None else (lambda: [ref(j) for j in range(16)]), 5, 2) / 16 * 1e3
+            out[f"layout{layout}"]["entry"] = "nwc_gather_xindex" if c.row_index() is not None else "nwc_gather"
+            out[f"layout{layout}_nwc_gather"] = {"us": round(us2, 2),
+                                                 "entry": "nwc_gather (reference signature, no row index)"}
+            del g2
         del c, g
         torch.cuda.empty_cache()
     return {"metric": f"embedding gather of {n} ids from a 152064x3584 compressed table, us per call",

@@ -125,6 +125,16 @@ int nwc_gather(void *stream, const uint8_t *data, const uint32_t *bases, const u
                const uint8_t *low, const int64_t *ids, uint32_t n_ids, uint16_t *out, uint64_t n, uint32_t block,
                uint32_t K, int elem);
 
+/* nwc_gather for layouts 0/1 with the row index (from nwc_row_index) and, optionally, the 13-bit table (nwc_seq_table;
+ * NULL: the stored LUT).  Layout 0: decoding starts at the row pair that holds each row, so a lookup decodes at most
+ * two rows of each block instead of up to eight.  Layout 1: four half-waves per block, each from the index's start of
+ * its quarter of the super-chunks.  Same output, bit for bit; ids outside [0, M) leave their row untouched.  -1 for
+ * layout 2, a missing row_index or a bad shape; 0 for n_ids == 0.  No counterpart in the reference (its lookup is
+ * nwc_gather, nwc_ops.cu:1143). */
+int nwc_gather_xindex(void *stream, const uint8_t *data, const uint32_t *bases, const uint8_t *hdr, const uint32_t *tab,
+                      const uint8_t *low, const uint16_t *row_index, const uint32_t *seq_table, const int64_t *ids,
+                      uint32_t n_ids, uint16_t *out, uint64_t n, uint32_t K, int elem);
+
 /* Uncompressed fp8 weight-only matvec (the bandwidth baseline): y = RNE_bf16(scale * (W8 x)), w fp8 e4m3fn [M x K]
  * row-major, scale fp32 [M], x fp32 [K16], y BF16 [M].  Replaces nwc_ops.cu:1163. */
 int nwc_ref_fp8(void *stream, const uint8_t *w, const float *scale, const float *x, uint16_t *y, uint64_t M, uint32_t K);

@@ -28,6 +28,7 @@ SIGNATURES = {
     "nwc_linear_xbf16": ("i", "ppppppppppppQIi"),
     "nwc_linear_xbf16_batch": ("i", "pppppppppppQIiI"),
     "nwc_prefill_xbf16": ("i", "ppppppppppppQIiI"),
+    "nwc_gather_xindex": ("i", "pppppppppIpQIi"),
     "nwc_seq_table": ("i", "pip"),
     "nwc_row_index": ("i", "pppppppQIi"),
     "nwc_token_split": ("i", "QIii"),

@@ -466,6 +466,18 @@ extern "C" int nwc_gather(void *stream, const uint8_t *data, const uint32_t *bas
     return layout == 2 ? launch_gather_fixed(t, a, (hipStream_t)stream) : launch_gather_prefix(layout, t, a, (hipStream_t)stream);
 }
 
+extern "C" int nwc_gather_xindex(void *stream, const uint8_t *data, const uint32_t *bases, const uint8_t *hdr,
+                                 const uint32_t *tab, const uint8_t *low, const uint16_t *row_index,
+                                 const uint32_t *seq_table, const int64_t *ids, uint32_t n_ids, uint16_t *out, uint64_t n,
+                                 uint32_t K, int elem) {
+    const int layout = elem_layout(elem);
+    if (!shape_ok(n, kBlock, K, elem) || layout > 1 || !row_index) return -1;
+    if (n_ids == 0) return 0;
+    if (current_cus() <= 0) return (int)hipErrorNoDevice;
+    GatherArgs a{data, bases, hdr, tab, low, ids, n_ids, out, (uint32_t)(n / K), K, slot_words_for(layout)};
+    return launch_gather0x(layout, elem_type(elem), a, row_index, seq_table, (hipStream_t)stream);
+}
+
 extern "C" int nwc_ref_fp8(void *stream, const uint8_t *w, const float *scale, const float *x, uint16_t *y, uint64_t M, uint32_t K) {
     if (M == 0 || K == 0 || M > 0xFFFFFFFFull) return -1;
     const int ncu = current_cus();

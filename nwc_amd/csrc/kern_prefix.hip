@@ -1328,6 +1328,133 @@ int launch_gather_prefix(int layout, int elem_t, const GatherArgs &a, hipStream_
     return (int)hipGetLastError();
 }
 
+// Layout-0 row gather with the row index (nwc_gather_xindex): one half-wave per (id, column block), as k_gather0, but
+// the cursor starts at the row pair that holds the row (the index's bit position of row 2j, j = (row % 8) / 2), so a
+// half-wave decodes one or two rows (four or eight steps) instead of up to eight, with the token path's cursor and
+// table (13-bit with `seq`, else the stored LUT re-encoded).  Out-of-range ids leave their output rows untouched.
+template <int ELEM, int PEEK>
+__global__ void __launch_bounds__(256) k_gather0x(GatherArgs a, const uint16_t *__restrict__ aux,
+                                                 const uint32_t *__restrict__ seq) {
+    __shared__ LutT<PEEK> s;
+    extern __shared__ uint32_t dyn[];
+    BlockArgs ta{};
+    ta.lut = a.lut;
+    ta.seq = seq;
+    TabStage<PEEK> Q;
+    Q.issue(ta);
+    const uint32_t L = threadIdx.x & 31, hw = threadIdx.x >> 5;
+    uint32_t *slot = dyn + hw * a.slot_words;
+    const Shape f(a.M, a.K, 0);
+    const uint32_t item = blockIdx.x * (blockDim.x >> 5) + hw, id = item / f.CB, cb = item - id * f.CB;
+    Q.commit(s);
+    Q.finish(s, ta);
+    __syncthreads();                                              // every thread stages the table first
+    if (id >= a.n_ids) return;
+    const int64_t R = a.ids[id];
+    if (R < 0 || R >= (int64_t)a.M) return;
+    const uint32_t rb = (uint32_t)R / kRows0, rr = (uint32_t)R % kRows0;
+    const uint32_t b = rb * f.CB + cb, col0 = cb * kCols + L * 16;
+    const bool col_ok = col0 < f.K16;
+    const LaneSpan sp = lane_span(a.hdr, b, L);
+    const uint32_t base = a.bases[b];
+    const uint4 raw = raw_row0<ELEM>(a.low, f, (uint32_t)R, col0, col_ok);
+    const uint32_t P = rr >= 2u ? aux[((uint64_t)b * kRowIndexSplits + (rr >> 1) - 1u) * kLanes + L] : 0u;
+    uint32_t sh;
+    const bool staged = stage_block(slot, a.slot_words, a.data, base, sp.total, L, sh);
+    const uint32_t *words = staged ? (const uint32_t *)slot + sh + sp.start : (const uint32_t *)(a.data + base) + sp.start;
+    Seq<ELEM> S;
+    S.init_at(words, P);
+    const XRegs<true> xnone{};
+    uint32_t pw[8];
+    if (rr & 1u) row0<ELEM, kDequant, true>(S, s, raw, xnone, pw);    // the pair's first row, decoded past
+    row0<ELEM, kDequant, true>(S, s, raw, xnone, pw);
+    if (col_ok) {
+        uint4 *op = (uint4 *)(a.out + (uint64_t)id * f.K16 + col0);
+        op[0] = make_uint4(pw[0], pw[1], pw[2], pw[3]);
+        op[1] = make_uint4(pw[4], pw[5], pw[6], pw[7]);
+    }
+}
+
+// Layout 1: four half-waves per (id, column block), each decoding a quarter of the block's super-chunks (4p .. 4p + 3)
+// from the row index's bit position of super-chunk 4p: 16 steps on the chain instead of up to 64.  Lanes whose row
+// r = L / 4 (or r + 8) is the wanted one store its eight columns of each super-chunk, as k_gather1 does.
+template <int ELEM, int PEEK>
+__global__ void __launch_bounds__(256) k_gather1x(GatherArgs a, const uint16_t *__restrict__ aux,
+                                                 const uint32_t *__restrict__ seq) {
+    __shared__ LutT<PEEK> s;
+    extern __shared__ uint32_t dyn[];
+    BlockArgs ta{};
+    ta.lut = a.lut;
+    ta.seq = seq;
+    TabStage<PEEK> Q;
+    Q.issue(ta);
+    constexpr uint32_t RB = ELEM == kElemFp8 ? 8u : 16u;
+    const uint32_t L = threadIdx.x & 31, r = L >> 2, q = L & 3, hw = threadIdx.x >> 5;
+    uint32_t *slot = dyn + hw * a.slot_words;
+    const Shape f(a.M, a.K, 1);
+    const uint32_t item = blockIdx.x * (blockDim.x >> 5) + hw, pair = item >> 2, p = item & 3u;
+    const uint32_t id = pair / f.CB, cb = pair - id * f.CB;
+    Q.commit(s);
+    Q.finish(s, ta);
+    __syncthreads();                                              // every thread stages the table first
+    if (id >= a.n_ids) return;
+    const int64_t R = a.ids[id];
+    if (R < 0 || R >= (int64_t)a.M) return;
+    const uint32_t rb = (uint32_t)R / kRows12, rr = (uint32_t)R % kRows12;
+    const uint32_t nsc = ((cb == f.CB - 1 ? f.nl : 32u) + 1) / 2, sc0 = 4u * p;
+    if (sc0 >= nsc) return;
+    const uint32_t ns = min(4u, nsc - sc0), b = rb * f.CB + cb;
+    const bool mine = (rr & 7u) == r, upper = rr >= 8;
+    const uint8_t *rp = a.low + ((uint64_t)(rb * f.spr + cb * 16 + sc0) * kLanes + L) * RB;
+    const LaneSpan sp = lane_span(a.hdr, b, L);
+    const uint32_t base = a.bases[b];
+    const uint32_t P = p ? aux[((uint64_t)b * kRowIndexSplits + p - 1u) * kLanes + L] : 0u;
+    uint32_t sh;
+    const bool staged = stage_block(slot, a.slot_words, a.data, base, sp.total, L, sh);
+    const uint32_t *words = staged ? (const uint32_t *)slot + sh + sp.start : (const uint32_t *)(a.data + base) + sp.start;
+    Seq<ELEM> S;
+    S.init_at(words, P);
+    uint16_t *o = a.out + (uint64_t)id * f.K16;
+    for (uint32_t i = 0; i < ns; i++) {
+        const uint4 raw = raw_slot1<ELEM>(rp + (uint64_t)i * kLanes * RB);
+        uint32_t v[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const uint32_t s0 = S.s;
+            const uint32_t *wp0 = S.wp;
+            uint32_t e1, e2;
+            if (__any(S.fast_quad(s, e1, e2) >= kSeqSlowTest)) {
+                S.s = s0;
+                S.wp = wp0;
+                S.reload();
+                S.slow_quad(s, e1, e2);
+            }
+            const uint32_t rk = u4_get(raw, k);
+            v[k] = upper ? perm(e2, rk, kSelPair2) : perm(e1, rk, kSelPair0);
+        }
+        const uint32_t kc = cb * kCols + (sc0 + i) * 32 + 8 * q;
+        if (mine && kc < f.K16) *(uint4 *)(o + kc) = make_uint4(v[0], v[1], v[2], v[3]);
+    }
+}
+
+int launch_gather0x(int layout, int elem_t, const GatherArgs &a, const uint16_t *aux, const uint32_t *seq, hipStream_t st) {
+    const uint32_t per = 8;                                        // half-wave items per 256-thread workgroup
+    const uint64_t items = (uint64_t)a.n_ids * Shape(a.M, a.K, layout).CB * (layout == 1 ? 4u : 1u);
+    const dim3 grid((uint32_t)((items + per - 1) / per));
+    const size_t lds = (size_t)per * a.slot_words * 4;
+#define NWC_GX(K_, E, T) hipLaunchKernelGGL((K_<E, T>), grid, dim3(256), lds, st, a, aux, seq)
+    const bool fp8 = elem_t == kElemFp8;
+    if (layout == 1) {
+        if (seq) { if (fp8) NWC_GX(k_gather1x, kElemFp8, kPeekSeq); else NWC_GX(k_gather1x, kElemBf16, kPeekSeq); }
+        else { if (fp8) NWC_GX(k_gather1x, kElemFp8, kPeek); else NWC_GX(k_gather1x, kElemBf16, kPeek); }
+    } else {
+        if (seq) { if (fp8) NWC_GX(k_gather0x, kElemFp8, kPeekSeq); else NWC_GX(k_gather0x, kElemBf16, kPeekSeq); }
+        else { if (fp8) NWC_GX(k_gather0x, kElemFp8, kPeek); else NWC_GX(k_gather0x, kElemBf16, kPeek); }
+    }
+#undef NWC_GX
+    return (int)hipGetLastError();
+}
+
 // ---------------------------------------------------------------------------------------------------------------
 // Prefill of a layout-0 matrix without a temporary BF16 copy: y[t] = W x[t] (+ bias, x scale) for T tokens.
 // A workgroup of 16 waves owns a tile of 64 rows (8 row groups) and TT tokens.  For each column block it decodes its

@@ -17,6 +17,8 @@ struct LaunchPlan {
 int launch_prefix(const LaunchPlan &p, int elem_t, int mode, bool xbf16, const BlockArgs &a, hipStream_t st);
 int launch_fixed(const LaunchPlan &p, int elem_t, int mode, bool xbf16, const BlockArgs &a, hipStream_t st);
 int launch_gather_prefix(int layout, int elem_t, const GatherArgs &a, hipStream_t st);
+// layouts 0/1 gather with the row index (k_gather0x / k_gather1x); seq: the 13-bit table or null
+int launch_gather0x(int layout, int elem_t, const GatherArgs &a, const uint16_t *aux, const uint32_t *seq, hipStream_t st);
 // layout-0 token path for ntok (2..4) activation vectors at once (k_layout0_batch); plan from plan_layout0_batch
 int launch_layout0_batch(const LaunchPlan &p, int elem_t, const BlockArgs &a, uint32_t ntok, hipStream_t st);
 int launch_gather_fixed(int elem_t, const GatherArgs &a, hipStream_t st);

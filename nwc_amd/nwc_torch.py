@@ -389,8 +389,13 @@ class NWCWeight:
         _need_gpu(self.data)
         flat = ids.reshape(-1).to(device=self.data.device, dtype=torch.int64).contiguous()
         rows = torch.empty(flat.numel(), self.K16, dtype=torch.bfloat16, device=self.data.device)
-        call("nwc_gather", stream(), *self._streams(), ptr(flat), flat.numel(), ptr(rows), self.n, self.block,
-             self.in_features, self.code)
+        index = self.row_index()
+        if index is not None:      # layouts 0/1: decode from the row index's starts (same rows, bit for bit)
+            call("nwc_gather_xindex", stream(), *self._streams(), ptr(index), ptr(self.seq_table()), ptr(flat),
+                 flat.numel(), ptr(rows), self.n, self.in_features, self.code)
+        else:
+            call("nwc_gather", stream(), *self._streams(), ptr(flat), flat.numel(), ptr(rows), self.n, self.block,
+                 self.in_features, self.code)
         if self.K16 != self.in_features:
             rows = rows[:, :self.in_features].contiguous()
         return rows.view(*ids.shape, self.in_features)

@@ -29,7 +29,8 @@ def test_header_declares_the_reference_exports():
     d = _declared()
     assert REFERENCE_EXPORTS <= d
     assert d - REFERENCE_EXPORTS == {"nwc_linear_xbf16", "nwc_linear_xbf16_batch", "nwc_row_index", "nwc_token_split",
-                                     "nwc_seq_table", "nwc_dequant_seq", "nwc_prefill_xbf16"}           # this build's additions
+                                     "nwc_seq_table", "nwc_dequant_seq", "nwc_prefill_xbf16",
+                                     "nwc_gather_xindex"}                                                 # this build's additions
 
 
 def test_library_exports_every_declared_symbol():
@@ -95,6 +96,8 @@ def _device_entry(lib):
     lib.nwc_linear_xbf16_batch.argtypes = [P, P, P, P, P, P, P, P, P, P, P, U64, U32, I, U32]
     lib.nwc_prefill_xbf16.restype = I
     lib.nwc_prefill_xbf16.argtypes = [P, P, P, P, P, P, P, P, P, P, P, P, U64, U32, I, U32]
+    lib.nwc_gather_xindex.restype = I
+    lib.nwc_gather_xindex.argtypes = [P, P, P, P, P, P, P, P, P, U32, P, U64, U32, I]
     return lib
 
 
@@ -119,6 +122,19 @@ def test_prefill_entry_point_refusals(elem, index, table, ntok, want):
     dummy = ctypes.c_void_p(8)
     args = [None] * 6 + [dummy if index else None, dummy if table else None] + [None] * 4
     assert lib.nwc_prefill_xbf16(*args, 2560 * 4096, 4096, elem, ntok) == want
+
+
+@pytest.mark.parametrize("elem,index,n_ids,want", [
+    (0x10, 0, 4, -1),           # layout 1 without the row index
+    (0x20, 1, 4, -1),           # layout 2
+    (0x00, 0, 4, -1),           # no row index
+    (0x00, 1, 0, 0),            # no ids: nothing to do
+])
+def test_gather_xindex_refusals(elem, index, n_ids, want):
+    """nwc_gather_xindex answers these before any device call (a dummy non-null row index is never dereferenced)."""
+    lib = _device_entry(_lib())
+    args = [None] * 6 + [ctypes.c_void_p(8) if index else None, None, None]
+    assert lib.nwc_gather_xindex(*args, n_ids, None, 2560 * 4096, 4096, elem) == want
 
 
 @pytest.mark.parametrize("M,K,elem,ok", [
@@ -150,3 +166,4 @@ def test_device_entry_points_refuse_unaddressable_planes(M, K, elem, ok):
     assert lib.nwc_linear_xbf16(None, *([None] * 11), n, K, elem) == -1
     assert lib.nwc_linear_xbf16_batch(None, *([None] * 10), n, K, elem, 2) == -1
     assert lib.nwc_prefill_xbf16(None, *([None] * 11), n, K, elem, 512) == -1
+    assert lib.nwc_gather_xindex(None, *([None] * 8), 4, None, n, K, elem) == -1

@@ -402,6 +402,38 @@ def test_reference_gather_shapes(cuda, layout, M, K):
     assert torch.equal(out[2, :K], w[0].view(torch.int16))
 
 
+@pytest.mark.parametrize("layout", [0, 1])
+@pytest.mark.parametrize("M,K,elem", [(1000, 2600, "bf16"), (300, 1000, "fp8"), (19, 40, "bf16"), (4096, 3584, "bf16")])
+def test_gather_xindex_matches_reference_entry_point(cuda, M, K, elem, layout):
+    """The row-index gather (layout 0: from the row pair that holds each row; layout 1: four half-waves per block, one
+    per quarter of the super-chunks) against the reference's entry point nwc_gather on the same ids, with the 13-bit
+    table and with the stored LUT: every row of a row group (ids 0..15 and random ones), ragged K (a last column block
+    of 40 or 16 columns), fp8, escapes; ids outside [0, M) leave their output rows untouched."""
+    NWCWeight, _, _ = _nwc()
+    from nwc_amd._abi import lib as _lib, ptr as _ptr, stream as _stream
+    print(f"gather xindex layout {layout} {M}x{K} {elem}", flush=True)
+    w = fp8_source(M, K, seed=M + K) if elem == "fp8" else bf16_matrix(M, K, seed=M + K, escapes=True)
+    c = NWCWeight(w, device="cuda", elem=elem, layout=layout)
+    if c.row_index() is None:
+        pytest.skip("no row index for this layout-1 shape")
+    g = torch.Generator().manual_seed(K)
+    ids = torch.cat([torch.arange(min(16, M)), torch.randint(0, M, (64,), generator=g), torch.tensor([-1, M, M + 9])])
+    ids = ids.cuda()
+    n = ids.numel()
+    ref = torch.full((n, c.K16), 0x1234, dtype=torch.int16, device="cuda")
+    assert _lib.nwc_gather(_stream(), _ptr(c.data), _ptr(c.bases), _ptr(c.hdr), _ptr(c.lut), _ptr(c.low), _ptr(ids), n,
+                           _ptr(ref), c.n, c.block, K, c.code) == 0
+    for table in (c.seq_table(), None):
+        out = torch.full((n, c.K16), 0x1234, dtype=torch.int16, device="cuda")
+        assert _lib.nwc_gather_xindex(_stream(), _ptr(c.data), _ptr(c.bases), _ptr(c.hdr), _ptr(c.lut), _ptr(c.low),
+                                      _ptr(c.row_index()), _ptr(table), _ptr(ids), n, _ptr(out), c.n, K, c.code) == 0
+        assert torch.equal(out.cpu(), ref.cpu())
+    torch.cuda.synchronize()
+    assert torch.all(ref[-3:].cpu() == 0x1234)
+    d = c.dequant().cpu().view(torch.int16)
+    assert torch.equal(ref[:-3, :K].cpu(), d[ids[:-3].cpu(), :K])
+
+
 def _random_shapes(n, seed):
     """Seeded log-uniform shapes (M up to 3000, K up to 20000): ragged K16/K32 tails, column-block counts from 1 to 40,
     row counts that leave partial row groups."""
