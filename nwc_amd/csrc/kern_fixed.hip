@@ -294,48 +294,67 @@ __global__ void __launch_bounds__(256) k_gather2(GatherArgs a) {
     constexpr uint32_t esz = ELEM == kElemFp8 ? 2u : 3u;
     const uint32_t L = threadIdx.x & 31, r = L >> 2, q = L & 3;
     const Shape f(a.M, a.K, 2);
-    // one half-wave per (id, column block): the blocks of a row decode in parallel
-    const uint32_t item = blockIdx.x * (blockDim.x >> 5) + (threadIdx.x >> 5), id = item / f.CB, cb = item - id * f.CB;
+    // four half-waves per (id, column block), each a quarter of its super-chunks (4p .. 4p + 3): the fixed-width planes
+    // need no cursor, so every super-chunk's loads go out together and a lookup waits one round trip, not sixteen
+    const uint32_t item = blockIdx.x * (blockDim.x >> 5) + (threadIdx.x >> 5), pair = item >> 2, p = item & 3u;
+    const uint32_t id = pair / f.CB, cb = pair - id * f.CB;
     if (id >= a.n_ids) return;
     const int64_t R = a.ids[id];
     if (R < 0 || R >= (int64_t)a.M) return;
+    const uint32_t nsc = ((cb == f.CB - 1 ? f.nl : 32u) + 1) / 2, sc0 = 4u * p;
+    if (sc0 >= nsc) return;
+    const uint32_t last = min(4u, nsc - sc0) - 1u;            // super-chunks past the block's last re-read it
     const uint8_t *rplane = a.low + f.nib2_bytes();
     const uint32_t rb = (uint32_t)R / kRows12, rr = (uint32_t)R % kRows12;
     const bool mine = (rr & 7u) == r, upper = rr >= 8;
     uint16_t *o = a.out + (uint64_t)id * f.K16;
-    {
-        const uint32_t nsc = ((cb == f.CB - 1 ? f.nl : 32u) + 1) / 2, slot0 = rb * f.spr + cb * 16;
-        const uint8_t *np = a.low + ((uint64_t)slot0 * kLanes + L) * 8;
-        const uint8_t *rp = ELEM == kElemFp8 ? rplane + (((uint64_t)rb * f.spr2 + cb * 8) * 3 * kLanes + L) * 4
-                                             : rplane + ((uint64_t)slot0 * kLanes + L) * 16;
-        for (uint32_t sc = 0; sc < nsc; sc++) {
-            const uint2 nib = *(const uint2 *)(np + (uint64_t)sc * kLanes * 8);
-            uint32_t p[4], qq[4];
-            if (ELEM == kElemFp8) {
-                const uint8_t *pp = rp + (uint64_t)(sc >> 1) * 3 * kLanes * 4;
-                const uint32_t c0 = *(const uint32_t *)pp, c1 = *(const uint32_t *)(pp + kLanes * 4), c2 = *(const uint32_t *)(pp + 2 * kLanes * 4);
-                if (sc & 1) decode_sc<ELEM, 4>(tab, &ms, nib, make_uint4(0, 0, 0, 0), c0, c1, c2, p, qq);
-                else decode_sc<ELEM, 0>(tab, &ms, nib, make_uint4(0, 0, 0, 0), c0, c1, c2, p, qq);
-            } else {
-                decode_sc<ELEM, 0>(tab, nullptr, nib, *(const uint4 *)(rp + (uint64_t)sc * kLanes * 16), 0u, 0u, 0u, p, qq);
-            }
-            const uint32_t kc = cb * kCols + sc * 32 + 8 * q;
-            if (mine && kc < f.K16) {
-                const uint32_t *v = upper ? qq : p;
-                *(uint4 *)(o + kc) = make_uint4(v[0], v[1], v[2], v[3]);
-            }
+    const uint32_t slot0 = rb * f.spr + cb * 16;
+    const uint8_t *np = a.low + ((uint64_t)(slot0 + sc0) * kLanes + L) * 8;
+    uint2 nib[4];
+    uint4 raw[4];
+    uint32_t c[2][3];
+#pragma unroll
+    for (uint32_t i = 0; i < 4; i++) nib[i] = *(const uint2 *)(np + (uint64_t)min(i, last) * kLanes * 8);
+    if constexpr (ELEM == kElemFp8) {                          // 3-bit fields per pair of super-chunks (sc0 is even)
+        const uint8_t *rp = rplane + (((uint64_t)rb * f.spr2 + cb * 8 + sc0 / 2u) * 3 * kLanes + L) * 4;
+#pragma unroll
+        for (uint32_t h = 0; h < 2; h++) {
+            const uint8_t *pp = rp + (uint64_t)min(h, last / 2u) * 3 * kLanes * 4;
+#pragma unroll
+            for (uint32_t w = 0; w < 3; w++) c[h][w] = *(const uint32_t *)(pp + w * kLanes * 4);
         }
-        // the whole half computes the prefix over the lanes' counts, only the row's lanes use it
-        const uint32_t b = rb * f.CB + cb;
-        const uint32_t cnt = a.hdr[(uint64_t)b * kHdrBytes + L];
-        const uint32_t incl = half_scan_incl(cnt, L);
-        const uint8_t *ep = a.data + a.bases[b] + (uint64_t)(incl - cnt) * esz;
-        if (mine) {
-            for (uint32_t k = 0; k < cnt; k++, ep += esz) {
-                const uint32_t i = ep[0], j = i & 15;
-                if ((((j >> 1) & 1u) != 0) != upper) continue;
-                o[cb * kCols + (i >> 4) * 32 + frag_col(L, j)] = (uint16_t)f32_to_bf16_rne(exc_value<ELEM>(ep));
-            }
+    } else {
+        const uint8_t *rp = rplane + ((uint64_t)(slot0 + sc0) * kLanes + L) * 16;
+#pragma unroll
+        for (uint32_t i = 0; i < 4; i++) raw[i] = *(const uint4 *)(rp + (uint64_t)min(i, last) * kLanes * 16);
+    }
+#pragma unroll
+    for (uint32_t i = 0; i < 4; i++) {
+        if (i > last) break;
+        uint32_t pv[4], qv[4];
+        if constexpr (ELEM == kElemFp8) {
+            if (i & 1u) decode_sc<ELEM, 4>(tab, &ms, nib[i], make_uint4(0, 0, 0, 0), c[i / 2][0], c[i / 2][1], c[i / 2][2], pv, qv);
+            else decode_sc<ELEM, 0>(tab, &ms, nib[i], make_uint4(0, 0, 0, 0), c[i / 2][0], c[i / 2][1], c[i / 2][2], pv, qv);
+        } else {
+            decode_sc<ELEM, 0>(tab, nullptr, nib[i], raw[i], 0u, 0u, 0u, pv, qv);
+        }
+        const uint32_t kc = cb * kCols + (sc0 + i) * 32 + 8 * q;
+        if (mine && kc < f.K16) {
+            const uint32_t *v = upper ? qv : pv;
+            *(uint4 *)(o + kc) = make_uint4(v[0], v[1], v[2], v[3]);
+        }
+    }
+    // exceptions of this lane in this quarter's super-chunks, after its plane values (the planes decode them to +-0);
+    // the whole half computes the prefix over the lanes' counts, only the row's lanes use it
+    const uint32_t b = rb * f.CB + cb;
+    const uint32_t cnt = a.hdr[(uint64_t)b * kHdrBytes + L];
+    const uint32_t incl = half_scan_incl(cnt, L);
+    const uint8_t *ep = a.data + a.bases[b] + (uint64_t)(incl - cnt) * esz;
+    if (mine) {
+        for (uint32_t k = 0; k < cnt; k++, ep += esz) {
+            const uint32_t i = ep[0], j = i & 15, sc = i >> 4;
+            if (sc - sc0 > last || (((j >> 1) & 1u) != 0) != upper) continue;
+            o[cb * kCols + sc * 32 + frag_col(L, j)] = (uint16_t)f32_to_bf16_rne(exc_value<ELEM>(ep));
         }
     }
 }
@@ -366,8 +385,8 @@ int launch_fixed(const LaunchPlan &p, int elem_t, int mode, bool xbf16, const Bl
 }
 
 int launch_gather_fixed(int elem_t, const GatherArgs &a, hipStream_t st) {
-    const uint32_t per = 8;                                        // (id, column block) items per workgroup
-    const uint64_t items = (uint64_t)a.n_ids * Shape(a.M, a.K, 2).CB;
+    const uint32_t per = 8;                                        // half-wave items per workgroup
+    const uint64_t items = (uint64_t)a.n_ids * Shape(a.M, a.K, 2).CB * 4u;
     const dim3 grid((uint32_t)((items + per - 1) / per));
     if (elem_t == kElemFp8) hipLaunchKernelGGL(k_gather2<kElemFp8>, grid, dim3(256), 0, st, a);
     else hipLaunchKernelGGL(k_gather2<kElemBf16>, grid, dim3(256), 0, st, a);

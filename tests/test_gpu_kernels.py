@@ -434,6 +434,33 @@ def test_gather_xindex_matches_reference_entry_point(cuda, M, K, elem, layout):
     assert torch.equal(ref[:-3, :K].cpu(), d[ids[:-3].cpu(), :K])
 
 
+@pytest.mark.parametrize("elem", ["bf16", "fp8"])
+def test_layout2_gather_exception_rows(cuda, elem):
+    """Layout 2's gather (four half-waves per block, each patching only the exceptions of its own super-chunks) on rows
+    dense in exceptions: a whole row, every third column of another, a run across a super-chunk boundary and the ragged
+    last column block; rows bit-exact against the original weights."""
+    NWCWeight, _, quantize_fp8 = _nwc()
+    M, K = 48, 1000
+    if elem == "fp8":
+        w = fp8_source(M, K, seed=3)
+        w[5] *= 40.0                                         # whole rows of outliers (exceptions after quantization)
+        w[21, ::3] *= 40.0
+        w[40, 500:520] *= 40.0
+        ref = quantize_fp8(w)[0].to(torch.bfloat16)
+    else:
+        w = bf16_matrix(M, K, seed=3, escapes=False)
+        sign = torch.tensor([1e30, -1e30], dtype=torch.bfloat16).repeat(K // 2)
+        w[5] = sign
+        w[21, ::3] = torch.tensor(1e30, dtype=torch.bfloat16)
+        w[40, 500:520] = torch.tensor(-1e30, dtype=torch.bfloat16)
+        w[40, 990:1000] = torch.tensor(3e29, dtype=torch.bfloat16)
+        ref = w
+    c = NWCWeight(w, device="cuda", elem=elem, layout=2)
+    ids = torch.tensor([5, 21, 40, 0, 47, 13, 29, 5, 40, 21, 8, 16])
+    print(f"layout-2 gather exception rows {elem}", flush=True)
+    assert torch.equal(c.gather(ids.cuda()).cpu().view(torch.int16), ref[ids].view(torch.int16))
+
+
 def _random_shapes(n, seed):
     """Seeded log-uniform shapes (M up to 3000, K up to 20000): ragged K16/K32 tails, column-block counts from 1 to 40,
     row counts that leave partial row groups."""
