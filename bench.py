@@ -179,8 +179,9 @@ def timed_steps(step, steps, warmup):
 
 def run_gpu(args, cfg, head=None):
     import torch
-    from nwc_amd.nwc_torch import NWCWeight, quantize_fp8, ref_fp8_matvec
+    from nwc_amd.nwc_torch import NWCWeight, quantize_fp8, ref_bf16_matvec, ref_fp8_matvec
     layers, shapes, elem, layout = cfg
+    light = getattr(args, "light", False)    # extra configs: sweep and per-shape graph times only
     torch.backends.cuda.preferred_blas_library("hipblaslt")
     dev = torch.device("cuda:0")
     props = torch.cuda.get_device_properties(dev)
@@ -240,10 +241,11 @@ def run_gpu(args, cfg, head=None):
         L = launches[name]
         g = graph_stack([(lambda j=j: L[j](cur())) for j in range(layers)])
         us = timed_steps(g.replay, 4, 1) / layers * 1e3 if g is not None else None
-        ev, _ = event_ms(lambda j: L[j](cur()), args.runs, layers)
+        ev = None if light else event_ms(lambda j: L[j](cur()), args.runs, layers)[0]
         nb = c.token_bytes() + 2 * K + 2 * M
-        per.append({"layer": name, "M": M, "K": K, "nwc_bytes": c.token_bytes(), "nwc_us": us, "nwc_us_event": ev * 1e3,
-                    "nwc_GBps": nb / (us * 1e-6) / 1e9 if us else None})
+        per.append({"layer": name, "M": M, "K": K, "nwc_bytes": c.token_bytes(), "nwc_us": us,
+                    "nwc_us_event": None if ev is None else ev * 1e3, "nwc_GBps": nb / (us * 1e-6) / 1e9 if us else None,
+                    "hbm_frac": nb / (us * 1e-6) / 1e9 / PEAK_HBM_GBS if us else None})
         del g
 
     # ---- roofline of the dominant kernel: average launch time of back-to-back gate_up launches (measured here,
@@ -277,8 +279,8 @@ def run_gpu(args, cfg, head=None):
         del hgraph
 
     # ---- hipBLASLt BF16 baseline: the same stack uncompressed ----
-    blas = fp8 = None
-    if not args.no_baseline:
+    blas = fp8 = bf16rows = None
+    if not args.no_baseline and not getattr(args, "no_blas", False):
         import torch.nn.functional as F
         wcopy = {name: [w.to(dev) for _ in range(layers)] for name, M, K, c, x, w in base}
         xs = {name: x.view(1, K) for name, M, K, c, x, w in base}
@@ -287,8 +289,8 @@ def run_gpu(args, cfg, head=None):
             W = wcopy[name]
             g = graph_stack([(lambda j=j: F.linear(xs[name], W[j])) for j in range(layers)])
             us = timed_steps(g.replay, 4, 1) / layers * 1e3 if g is not None else None
-            ev, _ = event_ms(lambda j: F.linear(xs[name], W[j]), args.runs, layers)
-            blas_per.append({"layer": name, "us": us, "us_event": ev * 1e3,
+            ev = None if light else event_ms(lambda j: F.linear(xs[name], W[j]), args.runs, layers)[0] * 1e3
+            blas_per.append({"layer": name, "us": us, "us_event": ev,
                              "GBps": (2 * M * K + 2 * K + 2 * M) / (us * 1e-6) / 1e9 if us else None})
             del g
 
@@ -298,6 +300,8 @@ def run_gpu(args, cfg, head=None):
                     F.linear(xs[name], wcopy[name][l])
         bgraph = graph_stack([bsweep])
         bms = timed_steps(bgraph.replay if bgraph is not None else bsweep, args.steps, args.warmup)
+        if elem == "bf16":
+            bf16rows = _bf16_rows_baseline(args, base, wcopy, layers, bf16_tok)
         blas = {"us_per_token_graph": bms * 1e3, "us_per_token_sum_of_launches": layers * sum(p["us"] for p in blas_per),
                 "GBps": bf16_tok / (bms * 1e-3) / 1e9, "per_layer": blas_per, "bytes_per_token": bf16_tok,
                 "library": "torch F.linear, preferred_blas_library=hipblaslt"}
@@ -320,6 +324,7 @@ def run_gpu(args, cfg, head=None):
             blas["us_per_token_with_lm_head"] = bhms * 1e3
             del g, bhgraph, hW, wcopy
         torch.cuda.empty_cache()
+    if not args.no_baseline:
         if elem == "fp8":
             # the library's uncompressed fp8 weight-only matvec on the same quantized weights (1 byte per weight)
             q8 = {}
@@ -369,9 +374,62 @@ def run_gpu(args, cfg, head=None):
     return {
         "ms_step": ms_step, "graph": graph is not None, "bytes_tok": bytes_tok, "bf16_tok": bf16_tok, "per": per,
         "sum_launch_us": sum_launch_us, "dom_bytes": dom_bytes, "dom_us": dom_ms * 1e3,
-        "achieved": dom_bytes / (dom_ms * 1e-3) / 1e9, "blas": blas, "fp8": fp8, "lm_head": lm,
+        "achieved": dom_bytes / (dom_ms * 1e-3) / 1e9, "blas": blas, "fp8": fp8, "lm_head": lm, "bf16rows": bf16rows,
         "device": {"name": props.name, "arch": props.gcnArchName, "cus": props.multi_processor_count},
     }
+
+
+def _bf16_rows_baseline(args, base, wcopy, layers, bf16_tok):
+    """The library's bandwidth-tuned uncompressed BF16 matvec (nwc_ref_bf16: the fp8 baseline's pattern at two bytes
+    per weight) over the same stack: per-shape graph times and the per-token sweep."""
+    from nwc_amd.nwc_torch import ref_bf16_matvec
+    per = []
+    for name, M, K, c, x, w in base:
+        W = wcopy[name]
+        us = avg_launch_ms(lambda j: ref_bf16_matvec(W[j], x), layers, 4) * 1e3
+        nb = 2 * M * K + 2 * K + 2 * M
+        per.append({"layer": name, "us": us, "GBps": nb / (us * 1e-6) / 1e9, "hbm_frac": nb / (us * 1e-6) / 1e9 / PEAK_HBM_GBS})
+
+    def sweep():
+        for l in range(layers):
+            for name, M, K, c, x, w in base:
+                ref_bf16_matvec(wcopy[name][l], x)
+    g = graph_stack([sweep])
+    ms = timed_steps(g.replay if g is not None else sweep, args.steps, args.warmup)
+    del g
+    return {"us_per_token_graph": ms * 1e3, "GBps": bf16_tok / (ms * 1e-3) / 1e9,
+            "hbm_frac": bf16_tok / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, "per_layer": per,
+            "library": "nwc_ref_bf16 (uncompressed BF16, 2 bytes per weight; k_bf16_rows: every load of a wave's rows in "
+                       "flight at once, v_dot2_f32_bf16, fp32 accumulation)"}
+
+
+def run_stream_ceiling(args, sizes_mb=(14.5, 21.8, 34.1, 68.0), copies=36):
+    """The read bandwidth a single launch of a given size reaches on this GPU: nwc_stream_read (every byte read once
+    with 16-byte non-temporal loads, one residency round of 256-thread workgroups) over `copies` distinct buffers per
+    size, graph-timed like the matvecs.  The sizes are the algorithmic bytes of the four Qwen3-4B matrices (o, qkv,
+    down, gate_up)."""
+    import torch
+    from nwc_amd._abi import call, ptr, stream
+    dev = torch.device("cuda:0")
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    grids = (cus, 2 * cus, 4 * cus, 8 * cus)
+    out = torch.empty(max(grids), dtype=torch.int32, device=dev)
+    rows = []
+    for mb in sizes_mb:
+        nbytes = int(mb * 1e6) // 16 * 16
+        bufs = [torch.empty(nbytes, dtype=torch.uint8, device=dev).fill_(i) for i in range(copies)]
+        per_grid = {}
+        for grid in grids:
+            per_grid[grid] = avg_launch_ms(lambda j: call("nwc_stream_read", stream(), ptr(bufs[j]), nbytes, ptr(out), grid),
+                                           copies, 4) * 1e3
+        grid, us = min(per_grid.items(), key=lambda kv: kv[1])
+        rows.append({"MB": mb, "us": round(us, 2), "GBps": round(nbytes / (us * 1e-6) / 1e9, 1),
+                     "hbm_frac": round(nbytes / (us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4), "grid": grid,
+                     "us_per_grid": {str(k): round(v, 2) for k, v in per_grid.items()}})
+        del bufs
+        torch.cuda.empty_cache()
+    return {"kernel": "k_stream_read (256-thread workgroups, 16-byte non-temporal loads, 8 in flight per thread; the "
+                      "fastest of 1, 2, 4 and 8 workgroups per CU)", "copies": copies, "per_size": rows}
 
 
 def run_prefill(args):
@@ -907,6 +965,76 @@ def run_encode(args):
             "speedup": round(t_ref / t_ours, 2)}
 
 
+def _sweep_summary(g, blas_ref=None):
+    """The per-token figures of one run_gpu result, for the extra-config keys of the driver line."""
+    us = g["ms_step"] * 1e3
+    gbps = g["bytes_tok"] / (us * 1e-6) / 1e9
+    out = {"us_per_token": round(us, 1), "GBps": round(gbps, 1), "hbm_frac": round(gbps / PEAK_HBM_GBS, 4),
+           "bytes_per_token": g["bytes_tok"],
+           "per_layer_us": {p["layer"]: round(p["nwc_us"], 2) for p in g["per"]},
+           "per_layer_hbm_frac": {p["layer"]: round(p["hbm_frac"], 4) for p in g["per"]}}
+    blas = g["blas"] or blas_ref
+    if blas is not None:
+        out["hipblaslt_us_per_token"] = round(blas["us_per_token_graph"], 1)
+        out["speedup_vs_hipblaslt"] = round(blas["us_per_token_graph"] / us, 3)
+    if g["bf16rows"] is not None:
+        out["uncompressed_bf16_tuned_us_per_token"] = round(g["bf16rows"]["us_per_token_graph"], 1)
+        out["speedup_vs_uncompressed_bf16_tuned"] = round(g["bf16rows"]["us_per_token_graph"] / us, 3)
+    return out
+
+
+def run_extras(args):
+    """Every other BASELINE config's figure in the default run (sweeps graph-timed as the headline is, without the
+    per-launch event timings): configs[1] Qwen3-0.6B layout 0; configs[2] Qwen3-4B layout 1; configs[3] Qwen3-4B fp8
+    layouts 0 and 1 against the uncompressed fp8 matvec; configs[4] Qwen2.5-7B layout 2; the 512-token Qwen3-4B
+    prefill (layout 0) and the 64-id embedding gather."""
+    import copy
+    import torch
+
+    def sub(**kw):
+        a = copy.copy(args)
+        a.light, a.no_cpu, a.no_baseline, a.no_blas = True, True, False, False
+        for k, v in kw.items():
+            setattr(a, k, v)
+        return a
+
+    def cfg(name, layout):
+        layers, shapes, elem, _, workload = CONFIGS[name]
+        return (layers, shapes, elem, layout), workload
+
+    out = {}
+    for key, name, layout, kw in (("qwen3_0.6b_layout0", "qwen3-0.6b", 0, {}),
+                                  ("qwen3_4b_layout1", "qwen3-4b", 1, {"no_blas": True}),
+                                  ("qwen3_4b_fp8_layout0", "qwen3-4b-fp8", 0, {"no_blas": True}),
+                                  ("qwen3_4b_fp8_layout1", "qwen3-4b-fp8", 1, {"no_baseline": True}),
+                                  ("qwen2.5_7b_layout2", "qwen2.5-7b-l2", 2, {})):
+        t0 = time.time()
+        c, workload = cfg(name, layout)
+        g = run_gpu(sub(**kw), c, None)
+        r = {"workload": f"{workload}, layout {layout}", **_sweep_summary(g)}
+        if g["fp8"] is not None:
+            r["native_fp8_us_per_token"] = round(g["fp8"]["us_per_token_graph"], 1)
+            r["native_fp8_per_layer_us"] = {p["layer"]: round(p["us"], 2) for p in g["fp8"]["per_layer"]}
+            out["_native_fp8"] = g["fp8"]["us_per_token_graph"]
+        if "fp8" in name and "_native_fp8" in out:
+            r["speedup_vs_native_fp8"] = round(out["_native_fp8"] / (g["ms_step"] * 1e3), 3)
+        out[key] = r
+        log(f"extra config {key}: {r['us_per_token']} us/token ({time.time() - t0:.1f} s)")
+        torch.cuda.empty_cache()
+    out.pop("_native_fp8", None)
+    t0 = time.time()
+    pf = run_prefill(sub(prefill=512, layout=0))
+    out["qwen3_4b_prefill512_layout0"] = {"us_per_stack": pf["per_stack"], "overhead_vs_resident": pf["overhead_vs_resident"],
+                                          "per_layer": pf["per_layer"]}
+    log(f"extra: prefill {pf['per_stack']} ({time.time() - t0:.1f} s)")
+    torch.cuda.empty_cache()
+    t0 = time.time()
+    ga = run_gather(sub(gather=64))
+    out["qwen2.5_7b_gather64"] = {"per_layout": ga["per_layout"], "unit": "us per call"}
+    log(f"extra: gather ({time.time() - t0:.1f} s)")
+    return out
+
+
 def traffic_bytes():
     """HBM bytes per gate_up launch from the committed rocprofv3 counter summary (FETCH_SIZE + WRITE_SIZE, each scaled
     by the factor a plain copy of known size gives), or None when there is none."""
@@ -957,6 +1085,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-baseline", action="store_true")
     ap.add_argument("--no-lm-head", action="store_true", help="skip the vocabulary matrix's timings")
+    ap.add_argument("--no-extras", action="store_true",
+                    help="default run: skip the other configs' sweeps, prefill, gather and the streaming ceiling")
     ap.add_argument("--profile-launches", type=int, default=0,
                     help="only run the counter target (copies + this many gate_up launches), for rocprofv3 --pmc")
     ap.add_argument("--profile-shape", default=DOMINANT, choices=[s[0] for s in SHAPES],
@@ -996,6 +1126,9 @@ def main():
     layers, shapes, elem, layout0, workload = CONFIGS[args.config]
     layout = args.layout if args.config in ("qwen3-4b", "qwen3-4b-fp8") else layout0
     g = run_gpu(args, (layers, shapes, elem, layout), None if args.no_lm_head else HEADS[args.config])
+    headline = args.config == "qwen3-4b" and layout == 0
+    extras = None if args.no_extras or not headline else run_extras(args)
+    ceiling = None if args.no_extras or not headline else run_stream_ceiling(args)
     cpu = None if args.no_cpu or args.config != "qwen3-4b" else run_cpu(args)
     us_tok = g["ms_step"] * 1e3
     value = g["bytes_tok"] / (g["ms_step"] * 1e-3) / 1e9
@@ -1034,6 +1167,9 @@ def main():
                     f"{HEADS[args.config][1]} vocabulary matvec, one HIP graph per token"},
         "hipblaslt": None if blas is None else rnd({**blas, "per_layer": [rnd(p) for p in blas["per_layer"]]}),
         "speedup_vs_hipblaslt": None if blas is None else round(blas["us_per_token_graph"] / us_tok, 3),
+        "uncompressed_bf16_tuned": None if g["bf16rows"] is None else rnd({**g["bf16rows"], "per_layer": [rnd(p) for p in g["bf16rows"]["per_layer"]]}),
+        "speedup_vs_uncompressed_bf16_tuned": None if g["bf16rows"] is None else round(g["bf16rows"]["us_per_token_graph"] / us_tok, 3),
+        "stream_ceiling": ceiling,
         "native_fp8": None if g["fp8"] is None else rnd({**g["fp8"], "per_layer": [rnd(p) for p in g["fp8"]["per_layer"]]}),
         "speedup_vs_native_fp8": None if g["fp8"] is None else round(g["fp8"]["us_per_token_graph"] / us_tok, 3),
         "roofline": {"bound": "hbm", "achieved": round(g["achieved"], 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
@@ -1047,6 +1183,7 @@ def main():
                                        "5 such measurements",
                      "sweep_achieved": round(g["bytes_tok"] / (g["sum_launch_us"] * 1e-6) / 1e9, 1)},
         "cpu_baseline": cpu,
+        "configs": extras,
         "device": g["device"],
     }
     print(json.dumps(line), flush=True)

@@ -11,7 +11,9 @@
  * Device entry points return 0, -1 for a shape the format cannot describe (or, in this build, a raw plane the
  * kernels cannot address with 32-bit offsets: layout 0 with Mp * K16 >= 2^32 for Mp = M rounded up to 8 rows,
  * layouts 1/2 with a plane of 2^32 - 512 bytes or more), or a hipError_t code of the launch.  `low` must be followed by the format's 512
- * slack bytes (nwc_torch.py:43); the kernels read into them.
+ * slack bytes (nwc_torch.py:43); the kernels read into them.  Activations (x, and the batched and prefill x
+ * matrices) must be 16-byte aligned: the kernels read them in 16-byte pieces (nwc_ref_fp8 and nwc_ref_bf16 accept
+ * any alignment).
  */
 #ifndef NWC_OPS_H
 #define NWC_OPS_H
@@ -138,6 +140,15 @@ int nwc_gather_xindex(void *stream, const uint8_t *data, const uint32_t *bases, 
 /* Uncompressed fp8 weight-only matvec (the bandwidth baseline): y = RNE_bf16(scale * (W8 x)), w fp8 e4m3fn [M x K]
  * row-major, scale fp32 [M], x fp32 [K16], y BF16 [M].  Replaces nwc_ops.cu:1163. */
 int nwc_ref_fp8(void *stream, const uint8_t *w, const float *scale, const float *x, uint16_t *y, uint64_t M, uint32_t K);
+
+/* Uncompressed BF16 matvec (a bandwidth baseline next to hipBLASLt): y = RNE_bf16(W x), w BF16 [M x K] row-major, x
+ * BF16 [K], y BF16 [M], fp32 accumulation.  No counterpart in the reference (its BF16 bar is cuBLAS through F.linear). */
+int nwc_ref_bf16(void *stream, const uint16_t *w, const uint16_t *x, uint16_t *y, uint64_t M, uint32_t K);
+
+/* Measurement kernel: `grid` workgroups read p[0 .. bytes) once (16-byte non-temporal loads, bytes a multiple of 16,
+ * p 16-byte aligned) and write one folded word each to out[0 .. grid).  The read bandwidth a launch of that size
+ * reaches.  No counterpart in the reference. */
+int nwc_stream_read(void *stream, const void *p, uint64_t bytes, uint32_t *out, uint32_t grid);
 
 /* Device set-up; returns the compute-unit count of the current device (0 without a usable GPU).  Called lazily by
  * the launchers.  Replaces nwc_ops.cu:1170. */

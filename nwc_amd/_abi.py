@@ -34,6 +34,8 @@ SIGNATURES = {
     "nwc_token_split": ("i", "QIii"),
     "nwc_gather": ("i", "pppppppIpQIIi"),
     "nwc_ref_fp8": ("i", "pppppQI"),
+    "nwc_ref_bf16": ("i", "ppppQI"),
+    "nwc_stream_read": ("i", "ppQpI"),
     "nwc_setup": ("i", ""),
 }
 

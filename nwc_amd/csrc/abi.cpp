@@ -356,6 +356,19 @@ int run_blocks(int mode, bool xbf16, hipStream_t st, const uint8_t *data, const 
 
 }  // namespace
 
+extern "C" int nwc_ref_bf16(void *stream, const uint16_t *w, const uint16_t *x, uint16_t *y, uint64_t M, uint32_t K) {
+    if (M == 0 || K == 0 || M > 0xFFFFFFFFull) return -1;
+    const int ncu = current_cus();
+    if (ncu <= 0) return (int)hipErrorNoDevice;
+    return launch_ref_bf16(w, x, y, (uint32_t)M, K, ncu, (hipStream_t)stream);
+}
+
+extern "C" int nwc_stream_read(void *stream, const void *p, uint64_t bytes, uint32_t *out, uint32_t grid) {
+    if (bytes == 0 || bytes % 16 != 0 || ((uintptr_t)p & 15u) != 0 || grid == 0) return -1;
+    if (current_cus() <= 0) return (int)hipErrorNoDevice;
+    return launch_stream_read(p, bytes, out, grid, (hipStream_t)stream);
+}
+
 extern "C" int nwc_setup(void) { return current_cus(); }
 
 extern "C" int nwc_matvec(void *stream, const uint8_t *data, const uint32_t *bases, const uint8_t *hdr, const uint32_t *tab,

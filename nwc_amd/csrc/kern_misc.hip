@@ -1,5 +1,7 @@
-// kern_misc.hip -- the uncompressed fp8 weight-only matvec (the "native fp8" bandwidth baseline the compressed fp8
-// path is compared with; counterpart of the reference's kern_ref_fp8, nwc_ops.cu:760-829).
+// kern_misc.hip -- the uncompressed baselines the compressed path is measured against: the fp8 weight-only matvec
+// (the "native fp8" baseline; counterpart of the reference's kern_ref_fp8, nwc_ops.cu:760-829), a BF16 matvec written
+// the same way (the uncompressed BF16 bar next to hipBLASLt), and a plain streaming read (the bandwidth a kernel of
+// a given size can reach on this GPU).
 //
 // Bandwidth-tuned: each workgroup streams a few whole rows with every lane keeping several 8-byte loads in flight,
 // converts with the gfx950 OCP-e4m3 packed conversion (v_cvt_pk_f32_fp8) and accumulates in fp32 against fp32
@@ -159,6 +161,138 @@ int launch_ref_fp8(const uint8_t *w, const float *scale, const float *x, uint16_
     const uint32_t jb = std::min(8u, (J + W - 1) / W);
     if (R == 8) launch_fp8_rows<8>(jb, dim3(groups), dim3(64 * W), st, w, scale, x, y, M, K);
     else launch_fp8_rows<4>(jb, dim3(groups), dim3(64 * W), st, w, scale, x, y, M, K);
+    return (int)hipGetLastError();
+}
+
+// ---- uncompressed BF16 matvec: y = RNE_bf16(W x), W BF16 [M x K] row-major, x BF16 [K] ----
+// The k_fp8_rows pattern at two bytes per weight: a workgroup owns R rows, its W waves split each row into chunks of
+// 512 columns (chunk j to wave j mod W), lane l owns columns 8l .. 8l + 7 of a chunk: one 16-byte non-temporal load
+// per row and one 16-byte load of x (shared by the R rows), JB chunks of every row in flight at once, x first.
+// v_dot2_f32_bf16 accumulates pairs in fp32; lane order, then a butterfly over the wave, then the waves in order.
+template <int R, int JB>
+__global__ void __launch_bounds__(512) k_bf16_rows(const uint16_t *__restrict__ w, const uint16_t *__restrict__ x,
+                                                   uint16_t *__restrict__ y, uint32_t M, uint32_t K) {
+    __shared__ float part[8][R];
+    const uint32_t lane = threadIdx.x & 63, wv = threadIdx.x >> 6, W = blockDim.x >> 6;
+    const uint32_t row0 = blockIdx.x * R, J = (K + 511u) >> 9;
+    const uint16_t *rp[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) rp[r] = w + (uint64_t)min(row0 + r, M - 1u) * K;
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) acc[r] = 0.f;
+    for (uint32_t j0 = wv; j0 < J; j0 += W * JB) {
+        uint4 q[JB][R], xv[JB];
+        bool ok[JB];
+        uint32_t cc[JB];
+#pragma unroll
+        for (int b = 0; b < JB; b++) {
+            const uint32_t c = (j0 + b * W) * 512u + 8u * lane;
+            ok[b] = j0 + b * W < J && c < K;
+            cc[b] = ok[b] ? c : 0u;
+            if (JB == 1 || j0 + b * W < J) xv[b] = *(const uint4 *)(x + cc[b]);      // wave-uniform branch
+        }
+#pragma unroll
+        for (int b = 0; b < JB; b++) {
+            if (JB == 1 || j0 + b * W < J) {
+#pragma unroll
+                for (int r = 0; r < R; r++) q[b][r] = ldnt4(rp[r] + cc[b]);
+            }
+        }
+#pragma unroll
+        for (int b = 0; b < JB; b++) {
+            if (JB > 1 && j0 + b * W >= J) break;
+            const uint4 xb = ok[b] ? xv[b] : make_uint4(0u, 0u, 0u, 0u);
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                acc[r] = dot2_bf16(q[b][r].x, xb.x, acc[r]);
+                acc[r] = dot2_bf16(q[b][r].y, xb.y, acc[r]);
+                acc[r] = dot2_bf16(q[b][r].z, xb.z, acc[r]);
+                acc[r] = dot2_bf16(q[b][r].w, xb.w, acc[r]);
+            }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < R; r++) acc[r] = wave_sum(acc[r]);
+    if (lane == 0) {
+#pragma unroll
+        for (int r = 0; r < R; r++) part[wv][r] = acc[r];
+    }
+    __syncthreads();
+    if (threadIdx.x < (uint32_t)R && row0 + threadIdx.x < M) {
+        float v = 0.f;
+        for (uint32_t i = 0; i < W; i++) v += part[i][threadIdx.x];
+        y[row0 + threadIdx.x] = (uint16_t)f32_to_bf16_rne(v);
+    }
+}
+
+// K % 8 != 0 or unaligned pointers: one wave per row, two bytes per lane and step.
+__global__ void __launch_bounds__(256) k_bf16_any(const uint16_t *__restrict__ w, const uint16_t *__restrict__ x,
+                                                  uint16_t *__restrict__ y, uint32_t M, uint32_t K) {
+    const uint32_t lane = threadIdx.x & 63, row = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    if (row >= M) return;
+    float acc = 0.f;
+    for (uint32_t k = lane; k < K; k += 64) acc = fmaf(bf16_lo(w[(uint64_t)row * K + k]), bf16_lo(x[k]), acc);
+    acc = wave_sum(acc);
+    if (lane == 0) y[row] = (uint16_t)f32_to_bf16_rne(acc);
+}
+
+template <int R>
+static void launch_bf16_rows(uint32_t jb, dim3 g, dim3 b, hipStream_t st, const uint16_t *w, const uint16_t *x,
+                             uint16_t *y, uint32_t M, uint32_t K) {
+    switch (jb) {
+    case 1: hipLaunchKernelGGL((k_bf16_rows<R, 1>), g, b, 0, st, w, x, y, M, K); break;
+    case 2: hipLaunchKernelGGL((k_bf16_rows<R, 2>), g, b, 0, st, w, x, y, M, K); break;
+    case 3: hipLaunchKernelGGL((k_bf16_rows<R, 3>), g, b, 0, st, w, x, y, M, K); break;
+    default: hipLaunchKernelGGL((k_bf16_rows<R, 4>), g, b, 0, st, w, x, y, M, K); break;
+    }
+}
+
+int launch_ref_bf16(const uint16_t *w, const uint16_t *x, uint16_t *y, uint32_t M, uint32_t K, int ncu, hipStream_t st) {
+    if ((K & 7u) != 0 || ((uintptr_t)w & 15u) != 0 || ((uintptr_t)x & 15u) != 0) {
+        hipLaunchKernelGGL(k_bf16_any, dim3((M + 3) / 4), dim3(256), 0, st, w, x, y, M, K);
+        return (int)hipGetLastError();
+    }
+    // as launch_ref_fp8, with the registers of a chunk in flight doubled (16-byte rows): R = 8 rows per workgroup
+    // for tall matrices with at most 2 chunks of each row in flight per wave, otherwise R = 4 with at most 4
+    const uint32_t R = M / 8u >= 4u * (uint32_t)ncu ? 8u : 4u, kWavesPerCu = 24u, jb_max = R == 8 ? 2u : 4u;
+    const uint32_t groups = (M + R - 1) / R, J = (K + 511u) / 512u;
+    const uint32_t W = std::max(1u, std::min({(kWavesPerCu * (uint32_t)ncu + groups - 1) / groups, J, 8u}));
+    const uint32_t jb = std::min(jb_max, (J + W - 1) / W);
+    if (R == 8) launch_bf16_rows<8>(jb, dim3(groups), dim3(64 * W), st, w, x, y, M, K);
+    else launch_bf16_rows<4>(jb, dim3(groups), dim3(64 * W), st, w, x, y, M, K);
+    return (int)hipGetLastError();
+}
+
+// ---- streaming read: the read bandwidth a launch of a given size reaches ----
+// Every workgroup reads a contiguous share of `bytes` (a multiple of 16) with 16-byte non-temporal loads, UNROLL of
+// them in flight per thread, folds the words with xor and writes one word: out[blockIdx.x].  The value only keeps
+// the loads alive.
+template <int UNROLL>
+__global__ void __launch_bounds__(256) k_stream_read(const uint4 *__restrict__ p, uint64_t n16, uint32_t *__restrict__ out) {
+    const uint64_t per = (n16 + gridDim.x - 1) / gridDim.x;
+    const uint64_t lo = (uint64_t)blockIdx.x * per, hi = min(lo + per, n16);
+    uint32_t v = 0;
+    for (uint64_t i = lo + threadIdx.x; i < hi; i += (uint64_t)blockDim.x * UNROLL) {
+        uint4 q[UNROLL];
+#pragma unroll
+        for (int u = 0; u < UNROLL; u++) {
+            const uint64_t j = i + (uint64_t)u * blockDim.x;
+            q[u] = ldnt4(p + (j < hi ? j : lo));
+        }
+#pragma unroll
+        for (int u = 0; u < UNROLL; u++) v ^= q[u].x ^ q[u].y ^ q[u].z ^ q[u].w;
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v ^= (uint32_t)__shfl_xor((int)v, o, 64);
+    __shared__ uint32_t red[4];
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    if (threadIdx.x == 0) out[blockIdx.x] = red[0] ^ red[1] ^ red[2] ^ red[3];
+}
+
+int launch_stream_read(const void *p, uint64_t bytes, uint32_t *out, uint32_t grid, hipStream_t st) {
+    hipLaunchKernelGGL(k_stream_read<8>, dim3(grid), dim3(256), 0, st, (const uint4 *)p, bytes / 16u, out);
     return (int)hipGetLastError();
 }
 

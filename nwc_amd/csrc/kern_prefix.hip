@@ -375,26 +375,33 @@ template <int PEEK> struct TabStage;
 // called after every request that must not wait for the streams (lut_finish says why)
 template <> struct TabStage<kPeek> {
     LutLoad Q;
-    __device__ __forceinline__ void issue(const BlockArgs &a) { lut_issue(Q, a.lut); }
-    __device__ __forceinline__ void commit(LutLds &s) { lut_commit<kLutSeq>(s, Q); }
-    __device__ __forceinline__ void finish(LutLds &s, const BlockArgs &a) { lut_finish<kLutSeq>(s, a.lut); }
+    __device__ __forceinline__ void issue(const BlockArgs &a, uint32_t nth = blockDim.x) { lut_issue(Q, a.lut, nth); }
+    __device__ __forceinline__ void commit(LutLds &s, uint32_t nth = blockDim.x) { lut_commit<kLutSeq>(s, Q, nth); }
+    __device__ __forceinline__ void finish(LutLds &s, const BlockArgs &a, uint32_t nth = blockDim.x) {
+        lut_finish<kLutSeq>(s, a.lut, nth);
+    }
 };
 template <> struct TabStage<kPeekSeq> {
     SeqLoad Q;
-    __device__ __forceinline__ void issue(const BlockArgs &a) { seq_issue(Q, a.seq); }
-    __device__ __forceinline__ void commit(LutLds13 &s) { seq_commit(s, Q); }
-    __device__ __forceinline__ void finish(LutLds13 &s, const BlockArgs &a) { seq_finish(s, a.seq); }
+    __device__ __forceinline__ void issue(const BlockArgs &a, uint32_t nth = blockDim.x) { seq_issue(Q, a.seq, nth); }
+    __device__ __forceinline__ void commit(LutLds13 &s, uint32_t nth = blockDim.x) { seq_commit(s, Q, nth); }
+    __device__ __forceinline__ void finish(LutLds13 &s, const BlockArgs &a, uint32_t nth = blockDim.x) {
+        seq_finish(s, a.seq, nth);
+    }
 };
 
-template <int ELEM, int MODE, bool XBF16, bool PIPE, int NR, int PEEK = kPeek>
-__global__ void __launch_bounds__(1024) k_layout0(BlockArgs a) {
+// nth: the workgroup's threads; flags: which of scale / bias are set (kFinishAll: read the pointers), for the token
+// kernel whose arguments the hardware preloads (k_layout0p) and which therefore reads neither blockDim nor those
+// pointers from memory before its first requests.
+template <int ELEM, int MODE, bool XBF16, bool PIPE, int NR, int PEEK>
+__device__ __forceinline__ void layout0_body(BlockArgs a, uint32_t nth, uint32_t flags) {
     static_assert(NR == 8 || ((NR == 4 || NR == 2) && !PIPE), "row splits only in the single-round kernel");
     static_assert(PEEK == kPeek || !PIPE, "the 13-bit table only in the single-round kernel");
     constexpr uint32_t SP = kRows0 / NR;                      // half-waves per block
     constexpr bool ROWS = MODE == kToken || MODE == kF32;     // modes that keep row sums
     __shared__ LutT<PEEK> s;
     extern __shared__ uint32_t dyn[];
-    const uint32_t tid = threadIdx.x, nth = blockDim.x, L = tid & 31;
+    const uint32_t tid = threadIdx.x, L = tid & 31;
     const uint32_t hw = tid >> 5, H = nth >> 5;
     const uint32_t HB = H / SP;                               // blocks per round
     const uint32_t cap = a.slot_words * HB;                   // words per region buffer
@@ -410,7 +417,7 @@ __global__ void __launch_bounds__(1024) k_layout0(BlockArgs a) {
     // and activations; loads complete in order, so each wait below covers only what it needs
     uint32_t t = hw / SP;
     const uint32_t r0 = (hw % SP) * NR;                       // first row of this half-wave's share of the block
-    const RowFinish fin = row_finish_load<MODE>(a, rg0 * kRows0, ng * kRows0);
+    const RowFinish fin = row_finish_load<MODE>(a, rg0 * kRows0, ng * kRows0, flags);
     Coord0 c = coord0(min(t, tl), rg0, f, L);
     Region R = region_of(a, B0, B0 + min(HB, nt), nb, mend);
     if constexpr (!PIPE) {
@@ -422,7 +429,7 @@ __global__ void __launch_bounds__(1024) k_layout0(BlockArgs a) {
         asm volatile("" : "+v"(c.rb));
     }
     TabStage<PEEK> Q;
-    Q.issue(a);
+    Q.issue(a, nth);
     uint32_t n = a.hdr[(uint64_t)c.b * kHdrBytes + L], base = a.bases[c.b];
     Bulk Bk;
     bulk_issue(Bk, a.data, R, tid, nth);
@@ -435,8 +442,8 @@ __global__ void __launch_bounds__(1024) k_layout0(BlockArgs a) {
         // they delay them: o_proj 8.1 -> 8.7 us, qkv 9.1 -> 9.6; after this wave's own chunks, before the barrier:
         // 4B sweep 0.2% slower)
         const uint32_t P0 = NR == 8 ? 0u : part_start(a, c.b, r0 >> 1, L);
-        Q.commit(s);
-        Q.finish(s, a);
+        Q.commit(s, nth);
+        Q.finish(s, a, nth);
         const bool fits = R.n16 * 4u <= cap;
         if (fits) bulk_commit(Bk, cur, R, tid, nth);
         uint4 raw[kRing0];
@@ -461,8 +468,8 @@ __global__ void __launch_bounds__(1024) k_layout0(BlockArgs a) {
         Coord0 cn = coord0(min(t + H, tl), rg0, f, L);
         uint32_t n_n = a.hdr[(uint64_t)cn.b * kHdrBytes + L], base_n = a.bases[cn.b];
         Region Rn = region_of(a, B0 + min(H, tl), B0 + min(2u * H, nt), nb, mend);
-        Q.commit(s);
-        Q.finish(s, a);
+        Q.commit(s, nth);
+        Q.finish(s, a, nth);
         if (R.n16 * 4u <= cap) bulk_commit(Bk, cur, R, tid, nth);
         __syncthreads();
         const uint32_t rounds = (nt + H - 1u) / H;
@@ -502,7 +509,34 @@ __global__ void __launch_bounds__(1024) k_layout0(BlockArgs a) {
             t += H;
         }
     }
-    if (ROWS) finish_rows<MODE>(a, part, rg0 * kRows0, ng * kRows0, f.CB, &fin);
+    if (ROWS) finish_rows<MODE>(a, part, rg0 * kRows0, ng * kRows0, f.CB, &fin, nth);
+}
+
+template <int ELEM, int MODE, bool XBF16, bool PIPE, int NR, int PEEK = kPeek>
+__global__ void __launch_bounds__(1024) k_layout0(BlockArgs a) {
+    layout0_body<ELEM, MODE, XBF16, PIPE, NR, PEEK>(a, blockDim.x, kFinishAll);
+}
+
+// The single-round token kernel (BF16 x, 13-bit table) with the inputs of its first requests as leading scalar
+// arguments, which gfx950 preloads into SGPRs (the library is built with -amdgpu-kernarg-preload-count): no wave waits
+// for a kernarg read before requesting the table, header bytes, activations and region bounds (4B sweep 1685 -> 1644
+// us per token).  pk = G | H << 16 | has_scale << 30 | has_bias << 31, H = the workgroup's half-waves; everything else
+// comes from `a`, whose copies of these fields are ignored.
+template <int ELEM, int NR>
+__global__ void __launch_bounds__(1024) k_layout0p(const uint32_t *__restrict__ bases, const uint32_t *__restrict__ seq,
+                                                   const uint8_t *__restrict__ hdr, const void *__restrict__ xp,
+                                                   uint32_t M, uint32_t K, uint32_t pk, const uint16_t *__restrict__ aux,
+                                                   BlockArgs a) {
+    a.bases = bases; a.seq = seq; a.hdr = hdr; a.x = xp; a.M = M; a.K = K; a.aux = aux;
+    a.G = pk & 0xFFFFu;
+    layout0_body<ELEM, kToken, true, false, NR, kPeekSeq>(a, ((pk >> 16) & 0x3FFFu) * 32u, pk >> 30);
+}
+
+template <int ELEM, int NR>
+static void launch_layout0p(const LaunchPlan &p, const BlockArgs &a, hipStream_t st) {
+    const uint32_t pk = p.G | ((p.threads / 32u) << 16) | (a.scale ? 1u << 30 : 0u) | (a.bias ? 1u << 31 : 0u);
+    hipLaunchKernelGGL((k_layout0p<ELEM, NR>), dim3(p.grid), dim3(p.threads), p.lds, st, a.bases, a.seq, a.hdr, a.x,
+                       a.M, a.K, pk, a.aux, a);
 }
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -790,13 +824,13 @@ __device__ __forceinline__ float2 chunks1_global(const Tab &s, const uint32_t *l
     return make_float2(accA, accB);
 }
 
-template <int ELEM, int MODE, bool XBF16, int NS, bool FULL, int PEEK = kPeek>
-__global__ void __launch_bounds__(1024) k_layout1s(BlockArgs a) {
+template <int ELEM, int MODE, bool XBF16, int NS, bool FULL, int PEEK>
+__device__ __forceinline__ void layout1s_body(BlockArgs a, uint32_t nth, uint32_t flags) {
     constexpr uint32_t SP = 16u / NS;                          // half-waves per block
     constexpr bool ROWS = MODE == kToken || MODE == kF32;
     __shared__ LutT<PEEK> s;
     extern __shared__ uint32_t dyn[];
-    const uint32_t tid = threadIdx.x, nth = blockDim.x, L = tid & 31;
+    const uint32_t tid = threadIdx.x, L = tid & 31;
     const uint32_t hw = tid >> 5;
     const Shape f(a.M, a.K, 1);
     const uint32_t cap = a.slot_words * a.G * f.CB;            // the plan's region: one slot per block of the tile
@@ -806,13 +840,13 @@ __global__ void __launch_bounds__(1024) k_layout1s(BlockArgs a) {
     float *part = (float *)(xs + (ROWS ? n8 : 0u));
     const uint32_t rg0 = blockIdx.x * a.G;
     const uint32_t ng = min(a.G, f.groups() - rg0);
-    const RowFinish fin = row_finish_load<MODE, ELEM == kElemFp8>(a, rg0 * kRows12, ng * kRows12);
+    const RowFinish fin = row_finish_load<MODE, ELEM == kElemFp8>(a, rg0 * kRows12, ng * kRows12, flags);
     const uint32_t nt = ng * f.CB, tl = nt - 1u;
     const uint32_t B0 = rg0 * f.CB, nb = f.nb;
     const uint32_t mend = B0 + nt == nb ? matrix_end(a, nb) : 0u;
     Region R = region_of(a, B0, B0 + nt, nb, mend);
     TabStage<PEEK> Q;
-    Q.issue(a);
+    Q.issue(a, nth);
     const uint32_t t = hw / SP, p = hw % SP, sc0 = p * NS;
     const Coord1 c = coord1<ELEM>(min(t, tl), rg0, f, L);
     const uint32_t n = a.hdr[(uint64_t)c.b * kHdrBytes + L], base = a.bases[c.b];
@@ -823,12 +857,12 @@ __global__ void __launch_bounds__(1024) k_layout1s(BlockArgs a) {
     // the raw chunks are requested once this wave's stream chunks are in, before the barrier (the first one is used
     // by the first decode step)
     const uint32_t P0 = SP == 1 ? 0u : part_start(a, c.b, sc0 / 4u, L);
-    Q.commit(s);
+    Q.commit(s, nth);
     if (ROWS) {
         x_commit<XBF16>(X, xs, n8, tid, nth);
         x_finish<XBF16>(xs, a.x, n8, tid, nth);
     }
-    Q.finish(s, a);
+    Q.finish(s, a, nth);
     // the copy moves four 16-byte chunks per thread (512 words per half-wave); a larger region (one half-wave per
     // block, as when the row index is built) decodes from global memory, except for dequantization, which copies the
     // rest of its region in a second pass
@@ -856,7 +890,23 @@ __global__ void __launch_bounds__(1024) k_layout1s(BlockArgs a) {
             part[pi + 8u * f.CB * SP] = v.y;                   // row r + 8
         }
     }
-    if (ROWS) finish_rows<MODE>(a, part, rg0 * kRows12, ng * kRows12, f.CB * SP, ELEM == kElemFp8 ? &fin : nullptr);
+    if (ROWS) finish_rows<MODE>(a, part, rg0 * kRows12, ng * kRows12, f.CB * SP, ELEM == kElemFp8 ? &fin : nullptr, nth);
+}
+
+template <int ELEM, int MODE, bool XBF16, int NS, bool FULL, int PEEK = kPeek>
+__global__ void __launch_bounds__(1024) k_layout1s(BlockArgs a) {
+    layout1s_body<ELEM, MODE, XBF16, NS, FULL, PEEK>(a, blockDim.x, kFinishAll);
+}
+
+// k_layout1s's token path with the inputs of its first requests preloaded into SGPRs (as k_layout0p).
+template <int ELEM, int NS, bool FULL, int PEEK>
+__global__ void __launch_bounds__(1024) k_layout1sp(const uint32_t *__restrict__ bases, const uint32_t *__restrict__ seq,
+                                                    const uint8_t *__restrict__ hdr, const void *__restrict__ xp,
+                                                    uint32_t M, uint32_t K, uint32_t pk, const uint16_t *__restrict__ aux,
+                                                    BlockArgs a) {
+    a.bases = bases; a.seq = seq; a.hdr = hdr; a.x = xp; a.M = M; a.K = K; a.aux = aux;
+    a.G = pk & 0xFFFFu;
+    layout1s_body<ELEM, kToken, true, NS, FULL, PEEK>(a, ((pk >> 16) & 0x3FFFu) * 32u, pk >> 30);
 }
 
 // Layout 1, several items per half-wave: for matrices whose row groups hold more blocks than a workgroup has
@@ -864,18 +914,18 @@ __global__ void __launch_bounds__(1024) k_layout1s(BlockArgs a) {
 // group (its streams staged once, up to ~90 KB of LDS), and its items (block, quarter of the super-chunks) go
 // round-robin to 32 half-waves; while an item decodes, the next item's raw super-chunks, header byte, base and
 // row-index entry are requested, so a half-wave never waits for global memory between items.
-template <int ELEM, bool FULL, int PEEK = kPeek>
-__global__ void __launch_bounds__(1024) k_layout1m(BlockArgs a) {
+template <int ELEM, bool FULL, int PEEK>
+__device__ __forceinline__ void layout1m_body(BlockArgs a, uint32_t nth, uint32_t flags) {
     constexpr int MODE = kToken;
     constexpr uint32_t NS = 4, SP = 4;
     __shared__ LutT<PEEK> s;
     extern __shared__ uint32_t dyn[];
-    const uint32_t tid = threadIdx.x, nth = blockDim.x, L = tid & 31;
+    const uint32_t tid = threadIdx.x, L = tid & 31;
     const uint32_t hw = tid >> 5, H = nth >> 5;
     const Shape f(a.M, a.K, 1);
     const uint32_t rg0 = blockIdx.x * a.G;
     const uint32_t ng = min(a.G, f.groups() - rg0);
-    const RowFinish fin = row_finish_load<MODE, ELEM == kElemFp8>(a, rg0 * kRows12, ng * kRows12);
+    const RowFinish fin = row_finish_load<MODE, ELEM == kElemFp8>(a, rg0 * kRows12, ng * kRows12, flags);
     const uint32_t nt = ng * f.CB;
     const uint32_t cap = a.slot_words * a.G * f.CB;
     const uint32_t n8 = (f.K16 + 31u) / 32u * 4u;
@@ -886,7 +936,7 @@ __global__ void __launch_bounds__(1024) k_layout1m(BlockArgs a) {
     const uint32_t mend = B0 + nt == nb ? matrix_end(a, nb) : 0u;
     Region R = region_of(a, B0, B0 + nt, nb, mend);
     TabStage<PEEK> Q;
-    Q.issue(a);
+    Q.issue(a, nth);
     const uint32_t ntot = nt * SP, itl = ntot - 1u;
     auto item = [&](uint32_t it, Coord1 &c, uint32_t &p) {
         const uint32_t i = min(it, itl);
@@ -907,8 +957,8 @@ __global__ void __launch_bounds__(1024) k_layout1m(BlockArgs a) {
     x_issue<true>(X, a.x, n8, tid, nth);
     x_commit<true>(X, xs, n8, tid, nth);
     x_finish<true>(xs, a.x, n8, tid, nth);
-    Q.commit(s);
-    Q.finish(s, a);
+    Q.commit(s, nth);
+    Q.finish(s, a, nth);
     uint4 ring[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) ring[i] = raw1<ELEM>(a.low, c, p * NS + i);
@@ -950,7 +1000,18 @@ __global__ void __launch_bounds__(1024) k_layout1m(BlockArgs a) {
         base = basen;
         P0 = P0n;
     }
-    finish_rows<MODE>(a, part, rg0 * kRows12, ng * kRows12, f.CB * SP, ELEM == kElemFp8 ? &fin : nullptr);
+    finish_rows<MODE>(a, part, rg0 * kRows12, ng * kRows12, f.CB * SP, ELEM == kElemFp8 ? &fin : nullptr, nth);
+}
+
+// The kernel, with the inputs of its first requests preloaded into SGPRs (as k_layout0p).
+template <int ELEM, bool FULL, int PEEK>
+__global__ void __launch_bounds__(1024) k_layout1mp(const uint32_t *__restrict__ bases, const uint32_t *__restrict__ seq,
+                                                    const uint8_t *__restrict__ hdr, const void *__restrict__ xp,
+                                                    uint32_t M, uint32_t K, uint32_t pk, const uint16_t *__restrict__ aux,
+                                                    BlockArgs a) {
+    a.bases = bases; a.seq = seq; a.hdr = hdr; a.x = xp; a.M = M; a.K = K; a.aux = aux;
+    a.G = pk & 0xFFFFu;
+    layout1m_body<ELEM, FULL, PEEK>(a, ((pk >> 16) & 0x3FFFu) * 32u, pk >> 30);
 }
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -1068,27 +1129,31 @@ __global__ void __launch_bounds__(256) k_gather1(GatherArgs a) {
 template <int ELEM, int PEEK>
 static int launch_layout1_token(const LaunchPlan &p, const BlockArgs &a, hipStream_t st, bool full) {
     const dim3 g(p.grid), b(p.threads);
+    // the preloaded kernels' packed word: tile, half-waves, scale and bias present
+    const uint32_t pk = p.G | ((p.threads / 32u) << 16) | (a.scale ? 1u << 30 : 0u) | (a.bias ? 1u << 31 : 0u);
+#define NWC_L1_PRELOAD a.bases, a.seq, a.hdr, a.x, a.M, a.K, pk, a.aux, a
     if (p.multi) {
         // more than 64 KB of LDS: raise the kernel's limit (idempotent, so concurrent first calls are fine)
-        auto kf = full ? (const void *)k_layout1m<ELEM, true, PEEK> : (const void *)k_layout1m<ELEM, false, PEEK>;
+        auto kf = full ? (const void *)k_layout1mp<ELEM, true, PEEK> : (const void *)k_layout1mp<ELEM, false, PEEK>;
         if (p.lds > 64u * 1024u) {
             const hipError_t e = hipFuncSetAttribute(kf, hipFuncAttributeMaxDynamicSharedMemorySize, (int)p.lds);
             if (e != hipSuccess) return (int)e;
         }
-        if (full) hipLaunchKernelGGL((k_layout1m<ELEM, true, PEEK>), g, b, p.lds, st, a);
-        else hipLaunchKernelGGL((k_layout1m<ELEM, false, PEEK>), g, b, p.lds, st, a);
+        if (full) hipLaunchKernelGGL((k_layout1mp<ELEM, true, PEEK>), g, b, p.lds, st, NWC_L1_PRELOAD);
+        else hipLaunchKernelGGL((k_layout1mp<ELEM, false, PEEK>), g, b, p.lds, st, NWC_L1_PRELOAD);
         return (int)hipGetLastError();
     }
-    if (p.split == 4) {
-        if (full) hipLaunchKernelGGL((k_layout1s<ELEM, kToken, true, 4, true, PEEK>), g, b, p.lds, st, a);
-        else hipLaunchKernelGGL((k_layout1s<ELEM, kToken, true, 4, false, PEEK>), g, b, p.lds, st, a);
+    if (p.split == 4 && p.G < 65536u) {
+        if (full) hipLaunchKernelGGL((k_layout1sp<ELEM, 4, true, PEEK>), g, b, p.lds, st, NWC_L1_PRELOAD);
+        else hipLaunchKernelGGL((k_layout1sp<ELEM, 4, false, PEEK>), g, b, p.lds, st, NWC_L1_PRELOAD);
         return (int)hipGetLastError();
     }
-    if (p.split == 2) {
-        if (full) hipLaunchKernelGGL((k_layout1s<ELEM, kToken, true, 8, true, PEEK>), g, b, p.lds, st, a);
-        else hipLaunchKernelGGL((k_layout1s<ELEM, kToken, true, 8, false, PEEK>), g, b, p.lds, st, a);
+    if (p.split == 2 && p.G < 65536u) {
+        if (full) hipLaunchKernelGGL((k_layout1sp<ELEM, 8, true, PEEK>), g, b, p.lds, st, NWC_L1_PRELOAD);
+        else hipLaunchKernelGGL((k_layout1sp<ELEM, 8, false, PEEK>), g, b, p.lds, st, NWC_L1_PRELOAD);
         return (int)hipGetLastError();
     }
+#undef NWC_L1_PRELOAD
     return -1;
 }
 
@@ -1133,6 +1198,14 @@ static int launch_prefix_t(const LaunchPlan &p, const BlockArgs &a, hipStream_t 
     if (p.layout == 0 && p.pipe) {
         hipLaunchKernelGGL((k_layout0<ELEM, MODE, XBF16, true, 8>), dim3(p.grid), dim3(p.threads), p.lds, st, a);
         return (int)hipGetLastError();
+    }
+    if constexpr (MODE == kToken && XBF16) {
+        if (p.layout == 0 && p.seq13 && !p.pipe && p.G < 65536u) {
+            if (p.split == 2) launch_layout0p<ELEM, 4>(p, a, st);
+            else if (p.split == 4) launch_layout0p<ELEM, 2>(p, a, st);
+            else launch_layout0p<ELEM, 8>(p, a, st);
+            return (int)hipGetLastError();
+        }
     }
     if constexpr ((MODE == kToken && XBF16) || MODE == kDequant) {
         if (p.layout == 0 && p.seq13 && !p.pipe) {

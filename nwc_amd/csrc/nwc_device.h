@@ -150,8 +150,8 @@ struct LutLoad {
     u32x4_t v0, v1, v2, v3;
     uint32_t ew;
 };
-__device__ __forceinline__ void lut_issue(LutLoad &Q, const uint32_t *__restrict__ lut) {
-    const uint32_t tid = threadIdx.x, nth = blockDim.x;
+__device__ __forceinline__ void lut_issue(LutLoad &Q, const uint32_t *__restrict__ lut, uint32_t nth = blockDim.x) {
+    const uint32_t tid = threadIdx.x;
     constexpr uint32_t n4 = kLutWords / 4;
     // source word of exp_of_rank[q]: pattern "q zeros, one, sign 0" for q < 11; ranks 11-14 sit in bytes 1/2 of
     // entries 0 and 1 (11, 13: byte 1; 12, 14: byte 2); slot 15 is unused
@@ -170,8 +170,8 @@ __device__ __forceinline__ void lut_store4(LutLds &s, uint32_t i, u32x4_t e) {
     ((u32x4_t *)s.tab)[i] = e;
 }
 template <int KIND>
-__device__ __forceinline__ void lut_commit(LutLds &s, const LutLoad &Q) {
-    const uint32_t tid = threadIdx.x, nth = blockDim.x;
+__device__ __forceinline__ void lut_commit(LutLds &s, const LutLoad &Q, uint32_t nth = blockDim.x) {
+    const uint32_t tid = threadIdx.x;
     constexpr uint32_t n4 = kLutWords / 4;
     if (tid < n4) lut_store4<KIND>(s, tid, Q.v0);
     if (tid + nth < n4) lut_store4<KIND>(s, tid + nth, Q.v1);
@@ -181,8 +181,8 @@ __device__ __forceinline__ void lut_commit(LutLds &s, const LutLoad &Q) {
     if (tid < 16) s.eor[tid] = q == 15u ? 0 : (uint8_t)((Q.ew >> ((q < 11u || (q & 1u)) ? 8u : 16u)) & 0x7Fu);
 }
 template <int KIND>
-__device__ __forceinline__ void lut_finish(LutLds &s, const uint32_t *__restrict__ lut) {
-    const uint32_t tid = threadIdx.x, nth = blockDim.x;
+__device__ __forceinline__ void lut_finish(LutLds &s, const uint32_t *__restrict__ lut, uint32_t nth = blockDim.x) {
+    const uint32_t tid = threadIdx.x;
     constexpr uint32_t n4 = kLutWords / 4;
     for (uint32_t i = tid + 4u * nth; i < n4; i += nth) lut_store4<KIND>(s, i, ((const u32x4_t *)lut)[i]);   // < 256 threads
 }
@@ -205,8 +205,8 @@ __device__ __forceinline__ uint32_t lds_entry(const LutT<PEEK> &s, uint32_t byte
 struct SeqLoad {
     u32x4_t v0, v1, v2;
 };
-__device__ __forceinline__ void seq_issue(SeqLoad &Q, const uint32_t *__restrict__ tab) {
-    const uint32_t tid = threadIdx.x, nth = blockDim.x;
+__device__ __forceinline__ void seq_issue(SeqLoad &Q, const uint32_t *__restrict__ tab, uint32_t nth = blockDim.x) {
+    const uint32_t tid = threadIdx.x;
     constexpr uint32_t n4 = kSeqTableWords / 4;
     const u32x4_t *t4 = (const u32x4_t *)tab;
     Q.v0 = t4[min(tid, n4 - 1u)];
@@ -218,15 +218,15 @@ __device__ __forceinline__ void seq_store(LutLds13 &s, uint32_t i, u32x4_t v) {
     if (i < n4 - 1u) ((u32x4_t *)s.tab)[i] = v;
     else if (i == n4 - 1u) *(u32x4_t *)s.eor = v;                      // the last chunk: exp_of_rank
 }
-__device__ __forceinline__ void seq_commit(LutLds13 &s, const SeqLoad &Q) {
-    const uint32_t tid = threadIdx.x, nth = blockDim.x;
+__device__ __forceinline__ void seq_commit(LutLds13 &s, const SeqLoad &Q, uint32_t nth = blockDim.x) {
+    const uint32_t tid = threadIdx.x;
     seq_store(s, tid, Q.v0);
     seq_store(s, tid + nth, Q.v1);
     seq_store(s, tid + 2u * nth, Q.v2);
 }
 // the chunks past the first three per thread (fewer than 683 threads); called as lut_finish is
-__device__ __forceinline__ void seq_finish(LutLds13 &s, const uint32_t *__restrict__ tab) {
-    const uint32_t tid = threadIdx.x, nth = blockDim.x;
+__device__ __forceinline__ void seq_finish(LutLds13 &s, const uint32_t *__restrict__ tab, uint32_t nth = blockDim.x) {
+    const uint32_t tid = threadIdx.x;
     constexpr uint32_t n4 = kSeqTableWords / 4;
     for (uint32_t i = tid + 3u * nth; i < n4; i += nth) seq_store(s, i, ((const u32x4_t *)tab)[i]);
 }
@@ -488,16 +488,27 @@ constexpr uint32_t kRowIndexSplits = 3;
 // loads so that the finish does not wait a memory round trip for them (and so that no later wait covers them).
 // PRE = false loads nothing (kernels that keep the finish's own loads where a matrix rarely has either: the held
 // registers and the branch cost more there than the round trip).
+// The bias stays in its BF16 bits until the finish (widening it here would make the wave wait for the load).  `flags`
+// (bit 0: scale, bit 1: bias) says which pointers are set when a kernel knows it without reading them: kFinishAll
+// tests the pointers themselves.
 struct RowFinish {
-    float scale, bias;
+    float scale;
+    uint32_t bias_bits;
 };
+constexpr uint32_t kFinishAll = 0xFFFFFFFFu;
 template <int MODE, bool PRE = true>
-__device__ __forceinline__ RowFinish row_finish_load(const BlockArgs &a, uint32_t row0, uint32_t nrows) {
-    RowFinish r{1.f, 0.f};
+__device__ __forceinline__ RowFinish row_finish_load(const BlockArgs &a, uint32_t row0, uint32_t nrows,
+                                                     uint32_t flags = kFinishAll) {
+    RowFinish r{1.f, 0u};
     const uint32_t row = row0 + threadIdx.x;
     if (PRE && MODE == kToken && threadIdx.x < nrows && row < a.M) {
-        if (a.scale) r.scale = a.scale[row];
-        if (a.bias) r.bias = __uint_as_float((uint32_t)a.bias[row] << 16);
+        if (flags != kFinishAll) {
+            if (flags & 1u) r.scale = a.scale[row];
+            if (flags & 2u) r.bias_bits = a.bias[row];
+        } else {
+            if (a.scale) r.scale = a.scale[row];
+            if (a.bias) r.bias_bits = a.bias[row];
+        }
     }
     return r;
 }
@@ -507,9 +518,9 @@ __device__ __forceinline__ RowFinish row_finish_load(const BlockArgs &a, uint32_
 // bias, already loaded.
 template <int MODE>
 __device__ __forceinline__ void finish_rows(const BlockArgs &a, const float *part, uint32_t row0, uint32_t nrows, uint32_t CB,
-                                            const RowFinish *pre = nullptr) {
+                                            const RowFinish *pre = nullptr, uint32_t nth = blockDim.x) {
     __syncthreads();
-    for (uint32_t i = threadIdx.x; i < nrows; i += blockDim.x) {
+    for (uint32_t i = threadIdx.x; i < nrows; i += nth) {
         const uint32_t row = row0 + i;
         if (row >= a.M) break;
         float v = 0.f;
@@ -517,7 +528,7 @@ __device__ __forceinline__ void finish_rows(const BlockArgs &a, const float *par
         if (MODE == kToken) {
             const bool first = pre && i == threadIdx.x;
             if (a.scale) v *= first ? pre->scale : a.scale[row];
-            if (a.bias) v += first ? pre->bias : __uint_as_float((uint32_t)a.bias[row] << 16);
+            if (a.bias) v += __uint_as_float((first ? pre->bias_bits : (uint32_t)a.bias[row]) << 16);
             ((uint16_t *)a.out)[row] = (uint16_t)f32_to_bf16_rne(v);
         } else {
             ((float *)a.out)[row] = v;

@@ -26,5 +26,7 @@ int launch_gather_fixed(int elem_t, const GatherArgs &a, hipStream_t st);
 int launch_prefill0(int elem_t, uint32_t tt, const PrefillArgs &p, hipStream_t st);
 int launch_ref_fp8(const uint8_t *w, const float *scale, const float *x, uint16_t *y, uint32_t M, uint32_t K, int ncu,
                    hipStream_t st);
+int launch_ref_bf16(const uint16_t *w, const uint16_t *x, uint16_t *y, uint32_t M, uint32_t K, int ncu, hipStream_t st);
+int launch_stream_read(const void *p, uint64_t bytes, uint32_t *out, uint32_t grid, hipStream_t st);
 
 }  // namespace nwc

@@ -92,6 +92,17 @@ def ref_fp8_matvec(w8: torch.Tensor, scale: torch.Tensor, x_f32: torch.Tensor) -
     return y
 
 
+def ref_bf16_matvec(w: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
+    """Uncompressed BF16 matvec of the library (a bandwidth baseline next to hipBLASLt): BF16 y = RNE(W x), fp32
+    accumulation; w BF16 [out, in] row-major, x BF16 [in]."""
+    _need_gpu(w)
+    rows, cols = w.shape
+    y = torch.empty(rows, dtype=torch.bfloat16, device=w.device)
+    wc, xc = w.contiguous(), x.to(torch.bfloat16).contiguous()
+    call("nwc_ref_bf16", stream(), ptr(wc), ptr(xc), ptr(y), rows, cols)
+    return y
+
+
 def fits(out_features, in_features):
     """Whether the format can hold a matrix of this shape: any size, padded to whole blocks."""
     return out_features >= 1 and in_features >= 1
@@ -199,6 +210,7 @@ class NWCWeight:
         stored, length, geo = _encode(src, rows, cols, self.code)
         self._place(stored, scale, device, geo)
         self.bytes = self._stored_bytes(length)
+        self._derive()
 
     @staticmethod
     def _source(w, kind, scale):
@@ -245,6 +257,14 @@ class NWCWeight:
         _check_layout(layout)
         self._shape(out_f, in_f, block, kind, layout)
         geo = _geometry(out_f, in_f, self.code)
+        for name, t, dtype in (("data", data, torch.uint8), ("bases", bases, torch.int32), ("hdr", hdr, torch.uint8),
+                               ("lut", lut, torch.int32), ("low", low, torch.uint8)):
+            if t.dtype != dtype:
+                # the kernels read these bytes as u8 / u32 words: another dtype would move every offset and length
+                raise ValueError(f"checkpoint tensor {name} is {t.dtype}, expected {dtype}")
+        if kind == ELEM_FP8 and (scale is None or not scale.dtype.is_floating_point or scale.numel() != out_f):
+            raise ValueError("fp8 checkpoint needs a floating-point scale with one value per output row")
+        data, bases, hdr, lut, low = (t.reshape(-1).contiguous() for t in (data, bases, hdr, lut, low))
         if (bases.numel() != geo.blocks or hdr.numel() != geo.blocks * HDR_BLOCK or lut.numel() != TAB_WORDS
                 or low.numel() not in (geo.raw_bytes, geo.raw_bytes + RAW_SLACK)):
             raise ValueError("checkpoint does not match this library version")
@@ -253,6 +273,7 @@ class NWCWeight:
             low = F.pad(low, (0, RAW_SLACK))
         self._place({"data": data, "bases": bases, "hdr": hdr, "lut": lut, "low": low}, scale, device, geo)
         self.bytes = self._stored_bytes(self.data.numel())
+        self._derive()
         return self
 
     def tensors(self):
@@ -279,6 +300,21 @@ class NWCWeight:
         return ptr(self.data), ptr(self.bases), ptr(self.hdr), ptr(self.lut), ptr(self.low)
 
     # ---- derived structures (built once per matrix) ----
+    def _derive(self):
+        """Build the row index and the 13-bit table when the matrix is placed on a GPU, so that no later call, for
+        instance inside HIP-graph capture, has to build them."""
+        if self.data.device.type == "cuda" and not torch.cuda.is_current_stream_capturing():
+            self.row_index()
+            self.seq_table()
+
+    @staticmethod
+    def _not_capturing(what):
+        # a build recorded into a graph would not run before the graph is replayed, and the 13-bit table's host copy
+        # is not capturable: refuse rather than cache a tensor that was never written
+        if torch.cuda.is_available() and torch.cuda.is_current_stream_capturing():
+            raise RuntimeError(f"NWCWeight.{what}() is built on first use and cannot be built during HIP-graph capture; "
+                               f"call it once before capturing")
+
     def row_index(self):
         """uint16 [blocks x 3 x 32]: each lane's bit position at rows 2, 4, 6 (layout 0) or super-chunks 4, 8, 12
         (layout 1), built on the GPU on first use, so the token kernels can split a block over two or four
@@ -288,6 +324,7 @@ class NWCWeight:
             return None
         if self._row_index is None:
             _need_gpu(self.data)
+            self._not_capturing("row_index")
             index = torch.empty(self.bases.numel() * 3 * LANES, dtype=torch.int16, device=self.data.device)
             rc = lib.nwc_row_index(stream(), *self._streams(), ptr(index), self.n, self.in_features, self.code)
             if rc == -1 and self.layout == 1:
@@ -303,6 +340,7 @@ class NWCWeight:
         if self.layout > 1 or not SEQ_TABLE:
             return None
         if self._seq_table is None:
+            self._not_capturing("seq_table")
             table = torch.empty(SEQ_TABLE_WORDS, dtype=torch.int32)
             lut = self.lut.cpu().contiguous()
             if lib.nwc_seq_table(ptr(lut), self.code, ptr(table)):
@@ -374,7 +412,8 @@ class NWCWeight:
         if self.layout != 0:
             raise ValueError("prefill: layout 0 only")
         T = x.shape[0]
-        if self.K16 == self.in_features and x.dtype == torch.bfloat16 and x.is_contiguous():
+        if (self.K16 == self.in_features and x.dtype == torch.bfloat16 and x.is_contiguous()
+                and x.data_ptr() % 16 == 0):         # the kernel reads x in 16-byte pieces
             xin = x
         else:
             xin = torch.zeros(T, self.K16, dtype=torch.bfloat16, device=x.device)

@@ -30,7 +30,7 @@ def test_header_declares_the_reference_exports():
     assert REFERENCE_EXPORTS <= d
     assert d - REFERENCE_EXPORTS == {"nwc_linear_xbf16", "nwc_linear_xbf16_batch", "nwc_row_index", "nwc_token_split",
                                      "nwc_seq_table", "nwc_dequant_seq", "nwc_prefill_xbf16",
-                                     "nwc_gather_xindex"}                                                 # this build's additions
+                                     "nwc_gather_xindex", "nwc_ref_bf16", "nwc_stream_read"}              # this build's additions
 
 
 def test_library_exports_every_declared_symbol():

@@ -3,7 +3,7 @@
 and the checkpoint round trip with logits compared bit for bit (reference tests/test_nwc_torch.py,
 tests/test_checkpoint.py:28-56, tests/test_fp8.py).
 
-Bars: token path within one BF16 ulp of a float64 matvec on the decoded weights (+1e-5); 2-8 tokens of a layout-0
+Bars: token path rounded to nearest even from within 1e-3 |y| + 1e-5 of a float64 matvec on the decoded weights; 2-8 tokens of a layout-0
 matrix (the batched kernel) equal, token by token, to the single-token path; prefill (more tokens, or another layout)
 equal to F.linear on the original weights (the same GEMM on bit-identical operands); decoded weights and gathered rows
 bit-exact;
@@ -14,7 +14,7 @@ import pytest
 import torch
 import torch.nn.functional as F
 
-from tests.helpers import bf16_matrix, bits16, fp8_source, ref_matvec64
+from tests.helpers import bf16_matrix, bits16, check_rne, fp8_source, ref_matvec64, token_tol
 
 pytestmark = pytest.mark.gpu
 
@@ -46,8 +46,7 @@ def test_nwclinear_token_and_prefill(cuda, layout):
     y1 = lin(x1)
     assert y1.shape == (1, 1, M) and y1.dtype == torch.bfloat16
     y64 = ref_matvec64(bits16(w), x1.float().cpu().numpy().ravel(), bias_bits=bits16(b))
-    err = np.abs(y1.double().cpu().numpy().ravel() - y64)
-    assert np.all(err <= 2.0 ** -8 * np.abs(y64) + 1e-5)
+    check_rne(y1, y64, token_tol(y64))
     x5 = torch.randn(1, 5, K, generator=g).to(torch.bfloat16).cuda()
     y5 = lin(x5)
     if layout == 0:                         # the batched kernel: each token as the single-token path computes it
@@ -68,8 +67,7 @@ def test_nwclinear_fp8(cuda, layout):
     g = torch.Generator().manual_seed(5)
     x1 = torch.randn(1, K, generator=g).to(torch.bfloat16).cuda()
     y64 = ref_matvec64(bits16(q.to(torch.bfloat16)), x1.float().cpu().numpy().ravel(), scale=scale.numpy())
-    err = np.abs(lin(x1).double().cpu().numpy().ravel() - y64)
-    assert np.all(err <= 2.0 ** -8 * np.abs(y64) + 1e-5)
+    check_rne(lin(x1), y64, token_tol(y64))
     x3 = torch.randn(3, K, generator=g).to(torch.bfloat16).cuda()
     if layout == 0:                         # the batched kernel: each token as the single-token path computes it
         assert torch.equal(lin(x3), torch.cat([lin(x3[t:t + 1]) for t in range(3)]))
@@ -149,8 +147,7 @@ def test_ref_fp8_baseline_module(cuda):
     q, scale = quantize_fp8(w)
     x = torch.randn(1, K, generator=torch.Generator().manual_seed(2)).to(torch.bfloat16).cuda()
     y64 = ref_matvec64(bits16(q.to(torch.bfloat16)), x.float().cpu().numpy().ravel(), scale=scale.numpy())
-    err = np.abs(mod(x).double().cpu().numpy().ravel() - y64)
-    assert np.all(err <= 2.0 ** -8 * np.abs(y64) + 1e-5)
+    check_rne(mod(x), y64, token_tol(y64))
 
 
 def test_qwen2_checkpoint_round_trip_with_fp8(cuda, tmp_path):

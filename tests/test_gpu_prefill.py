@@ -1,16 +1,17 @@
 """GPU tests of the fused layout-0 prefill (nwc_prefill_xbf16, NWCWeight.prefill): several tokens multiplied with the
 compressed matrix without a temporary BF16 copy (decode into LDS, matrix cores).
 
-Bar: every output within one BF16 ulp of the float64 product on the decoded weights, plus the fp32 summation bound
-(2^-20 times the sum of |terms|) for the matrix cores' accumulation order: the kernel's sums are not in a GEMM
-library's order, so it matches F.linear to rounding, not bit for bit.  Covers ragged M and K (rows and columns past
+Bar: every output rounded once, to nearest even, from a value within 1e-3 |ref| + 1e-6 of the float64 product on the
+decoded weights, plus the fp32 summation bound (2^-20 times the sum of |terms|) for the matrix cores' accumulation
+order (tests/helpers.py check_rne): the kernel's sums are not in a GEMM library's order, so it matches F.linear to
+rounding, not bit for bit.  Covers ragged M and K (rows and columns past
 the matrix, a half k-step past K16), 1 to 512 tokens (all three token tiles and partial ones), BF16 with escapes, fp8
 with row scales, bias, and NWCLinear's opt-in dispatch (NWC_PREFILL=fused)."""
 import pytest
 import torch
 import torch.nn.functional as F
 
-from tests.helpers import bf16_matrix, fp8_source
+from tests.helpers import bf16_matrix, check_rne, fp8_source
 
 pytestmark = pytest.mark.gpu
 
@@ -29,9 +30,8 @@ def _check(c, x, y, bias):
     if bias is not None:
         ref = ref + bias.double()
     terms = x.double().abs() @ wd.abs().t()
-    bound = 2.0 ** -8 * ref.abs() + 2.0 ** -20 * terms + 1e-6
-    excess = ((y.double() - ref).abs() - bound).max().item()
-    assert excess <= 0, f"outside the bound by {excess:.3e}"
+    tol = 1e-3 * ref.abs() + 2.0 ** -20 * terms + 1e-6
+    check_rne(y, ref.cpu().numpy(), tol.cpu().numpy(), "prefill")
 
 
 @pytest.mark.parametrize("M,K,T,elem,with_bias", [

@@ -75,3 +75,26 @@ def test_wrong_sizes_refused():
         _rebuild(c, bases=c.bases[:-1].clone())
     with pytest.raises(ValueError):
         _rebuild(c, low=c.low[:-7].clone())
+
+
+@pytest.mark.parametrize("name,dtype", [("bases", torch.int64), ("hdr", torch.int32), ("lut", torch.int64),
+                                        ("data", torch.int8), ("low", torch.int16), ("bases", torch.float32)])
+def test_wrong_dtype_refused(name, dtype):
+    """The kernels read data/hdr/low as bytes and bases/lut as 32-bit words: a tensor of another dtype (values kept,
+    bytes reinterpreted) would move every offset and code length the validation checked, so it is refused."""
+    c = _weight(0)
+    t = getattr(c, name).clone()
+    if t.element_size() == torch.tensor([], dtype=dtype).element_size() and not dtype.is_floating_point:
+        t = t.view(dtype)
+    else:
+        t = t.to(dtype)
+    with pytest.raises(ValueError, match=name):
+        _rebuild(c, **{name: t})
+
+
+def test_fp8_needs_float_scale():
+    c = _weight(0, "fp8")
+    with pytest.raises(ValueError):
+        _rebuild(c, scale=c.scale.to(torch.int32))
+    with pytest.raises(ValueError):
+        _rebuild(c, scale=c.scale[:-1].clone())
