@@ -118,7 +118,8 @@ int nwc_row_index(void *stream, const uint8_t *data, const uint32_t *bases, cons
                   const uint8_t *low, uint16_t *row_index, uint64_t n, uint32_t K, int elem);
 
 /* Half-waves per block that nwc_linear_xbf16 would use on the current device (1, or 2 or 4 with a row index), for byte
- * accounting; -1 for a bad shape.  No counterpart in the reference. */
+ * accounting; with_row_index: bit 0 = a row index is passed, bit 1 = the 13-bit table is passed (plans differ with
+ * it); -1 for a bad shape.  No counterpart in the reference. */
 int nwc_token_split(uint64_t n, uint32_t K, int elem, int with_row_index);
 
 /* Rows ids[0..n_ids) -> BF16 [n_ids x K16] (embedding lookup from the compressed matrix); ids outside [0, M) leave

@@ -5,12 +5,22 @@
 
 #include <algorithm>
 #include <atomic>
+#include <cstdlib>
 
 using namespace nwc;
 
 namespace {
 
 constexpr int kMaxDevices = 64;
+
+// NWC_TAIL=0 turns the split-tail layout-0 token plan (k_layout0t) off, for comparisons; read once.
+bool tail_enabled() {
+    static const bool on = [] {
+        const char *v = getenv("NWC_TAIL");
+        return !(v && v[0] == '0');
+    }();
+    return on;
+}
 std::atomic<int> g_cus[kMaxDevices];
 
 int current_cus() {
@@ -65,8 +75,37 @@ constexpr uint32_t kDynLds13 = 47u * 1024u;
 // before any multi-round plan.
 enum Stage { kOneRound, kRounds, kRoundsOrPipe };
 bool plan_layout0_tiers(const Shape &f, int mode, int ncu, bool index, uint32_t budget, Stage stage, LaunchPlan &p);
+// Layout-0 token path with the row index and the 13-bit table, for matrices of one to two row groups per CU
+// (k_layout0t): one whole row group on each CU, the finest split of its blocks whose half-waves fit 32, and the rest
+// of the row groups cut into TS = 4 quarters (or 2 halves) of their rows, one workgroup each, so that every CU decodes
+// about the same rows: Qwen3-4B down (320 row groups: 256 whole + 256 quarters instead of two whole groups on 64
+// CUs) and o_proj (the same count).  Both kinds of workgroup share one launch shape: one half-wave per block and part.
+bool plan_layout0_tail(const Shape &f, int ncu, LaunchPlan &p) {
+    const uint32_t groups = f.groups(), CB = f.CB, n = (uint32_t)ncu;
+    if (groups <= n || CB > 32u) return false;
+    const uint32_t rest = groups - n;
+    const uint32_t ts = 4u * rest <= n ? 4u : 2u * rest <= n ? 2u : 0u;
+    if (ts == 0u || n > 65535u) return false;
+    const uint32_t split = 4u * CB <= 32u ? 4u : 2u * CB <= 32u ? 2u : 1u;
+    const uint32_t halves = (split * CB + 1u) & ~1u;
+    const uint32_t lds = CB * kSlotWords0 * 4u + kRows0 * CB * 4u;
+    if (lds > kDynLds13) return false;
+    p = LaunchPlan{};
+    p.layout = 0;
+    p.seq13 = true;
+    p.tail = ts;
+    p.split = split;
+    p.G = n;                                            // whole row groups (workgroups 0 .. n - 1)
+    p.threads = 32u * halves;
+    p.grid = n + ts * rest;
+    p.slot_words = kSlotWords0;
+    p.lds = lds;
+    return true;
+}
+
 bool plan_layout0(const Shape &f, int mode, int ncu, bool index, bool seq, LaunchPlan &p) {
     const bool t13 = seq && (mode == kToken || mode == kDequant);
+    if (mode == kToken && index && t13 && tail_enabled() && plan_layout0_tail(f, ncu, p)) return true;
     if (t13 && plan_layout0_tiers(f, mode, ncu, index, kDynLds13, kOneRound, p)) {
         p.seq13 = true;
         return true;
@@ -464,7 +503,8 @@ extern "C" int nwc_token_split(uint64_t n, uint32_t K, int elem, int with_row_in
     if (ncu <= 0) return (int)hipErrorNoDevice;
     const Shape f((uint32_t)(n / K), K, elem_layout(elem));
     LaunchPlan p;
-    if (!plan_blocks(f, elem_layout(elem), kToken, ncu, with_row_index != 0 && elem_layout(elem) <= 1, p)) return -1;
+    const bool index = (with_row_index & 1) != 0 && elem_layout(elem) <= 1, seq = (with_row_index & 2) != 0;
+    if (!plan_blocks(f, elem_layout(elem), kToken, ncu, index, p, seq && elem_layout(elem) <= 1)) return -1;
     return elem_layout(elem) <= 1 && p.split ? (int)p.split : 1;
 }
 

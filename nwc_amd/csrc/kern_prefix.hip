@@ -391,24 +391,26 @@ template <> struct TabStage<kPeekSeq> {
 };
 
 // nth: the workgroup's threads; flags: which of scale / bias are set (kFinishAll: read the pointers), for the token
-// kernel whose arguments the hardware preloads (k_layout0p) and which therefore reads neither blockDim nor those
-// pointers from memory before its first requests.
-template <int ELEM, int MODE, bool XBF16, bool PIPE, int NR, int PEEK>
-__device__ __forceinline__ void layout0_body(BlockArgs a, uint32_t nth, uint32_t flags) {
+// kernels whose arguments the hardware preloads (k_layout0p, k_layout0t) and which therefore read neither blockDim nor
+// those pointers from memory before their first requests.  rg0: the tile's first row group.  PART: the workgroup
+// decodes only rows NR jfix .. NR jfix + NR - 1 of its single row group (one half-wave per block, from the row
+// index's position), for the split tail of k_layout0t.  s / dyn: the kernel's table and dynamic LDS.
+template <int ELEM, int MODE, bool XBF16, bool PIPE, int NR, int PEEK, bool PART = false>
+__device__ __forceinline__ void layout0_body(BlockArgs a, uint32_t nth, uint32_t flags, uint32_t rg0, uint32_t jfix,
+                                             LutT<PEEK> &s, uint32_t *dyn) {
     static_assert(NR == 8 || ((NR == 4 || NR == 2) && !PIPE), "row splits only in the single-round kernel");
     static_assert(PEEK == kPeek || !PIPE, "the 13-bit table only in the single-round kernel");
-    constexpr uint32_t SP = kRows0 / NR;                      // half-waves per block
+    static_assert(!PART || (NR < 8 && !PIPE && MODE == kToken), "a row part of a single row group, token path");
+    constexpr uint32_t SP = PART ? 1u : kRows0 / NR;         // half-waves per block
     constexpr bool ROWS = MODE == kToken || MODE == kF32;     // modes that keep row sums
-    __shared__ LutT<PEEK> s;
-    extern __shared__ uint32_t dyn[];
     const uint32_t tid = threadIdx.x, L = tid & 31;
     const uint32_t hw = tid >> 5, H = nth >> 5;
     const uint32_t HB = H / SP;                               // blocks per round
-    const uint32_t cap = a.slot_words * HB;                   // words per region buffer
+    const Shape f(a.M, a.K, 0);
+    // words per region buffer: the tile's blocks (one round) or a round's (PIPE)
+    const uint32_t cap = a.slot_words * (PIPE ? HB : min(HB, a.G * f.CB));
     uint32_t *cur = dyn, *nxt = dyn + cap;
     float *part = (float *)(dyn + (PIPE ? 2u : 1u) * cap);
-    const Shape f(a.M, a.K, 0);
-    const uint32_t rg0 = blockIdx.x * a.G;
     const uint32_t ng = min(a.G, f.groups() - rg0);
     const uint32_t nt = ng * f.CB, tl = nt - 1u;              // look-ahead past the tile re-reads block tl
     const uint32_t B0 = rg0 * f.CB, nb = f.nb;
@@ -416,8 +418,9 @@ __device__ __forceinline__ void layout0_body(BlockArgs a, uint32_t nth, uint32_t
     // request order: region bounds and table first, then the stream copy (which needs the bounds), then the raw rows
     // and activations; loads complete in order, so each wait below covers only what it needs
     uint32_t t = hw / SP;
-    const uint32_t r0 = (hw % SP) * NR;                       // first row of this half-wave's share of the block
-    const RowFinish fin = row_finish_load<MODE>(a, rg0 * kRows0, ng * kRows0, flags);
+    const uint32_t r0 = PART ? NR * jfix : (hw % SP) * NR;    // first row of this half-wave's share of the block
+    const RowFinish fin = PART ? row_finish_load<MODE>(a, rg0 * kRows0 + r0, NR, flags)
+                               : row_finish_load<MODE>(a, rg0 * kRows0, ng * kRows0, flags);
     Coord0 c = coord0(min(t, tl), rg0, f, L);
     Region R = region_of(a, B0, B0 + min(HB, nt), nb, mend);
     if constexpr (!PIPE) {
@@ -459,7 +462,8 @@ __device__ __forceinline__ void layout0_body(BlockArgs a, uint32_t nth, uint32_t
                 v = rows0_global<ELEM, MODE, XBF16>(s, (const uint32_t *)(a.data + base) + start, a, f, x, c, true, L);
             else
                 v = rowsN_global<ELEM, MODE, XBF16, NR>(s, (const uint32_t *)(a.data + base) + start, P0, a, f, x, c, r0, L);
-            if (ROWS && (L & (4u * SP - 1u)) == 0) part[(c.g * kRows0 + r0 + L / (4u * SP)) * f.CB + c.cb] = v;
+            // lane 4r (NR = 8), 8r (4) or 16r (2) holds row r0 + r
+            if (ROWS && (L & (32u / NR - 1u)) == 0) part[(c.g * kRows0 + r0 + L / (32u / NR)) * f.CB + c.cb] = v;
         }
     } else {
         uint4 ring[4];
@@ -509,12 +513,15 @@ __device__ __forceinline__ void layout0_body(BlockArgs a, uint32_t nth, uint32_t
             t += H;
         }
     }
-    if (ROWS) finish_rows<MODE>(a, part, rg0 * kRows0, ng * kRows0, f.CB, &fin, nth);
+    if (PART) finish_rows<MODE>(a, part + r0 * f.CB, rg0 * kRows0 + r0, NR, f.CB, &fin, nth);
+    else if (ROWS) finish_rows<MODE>(a, part, rg0 * kRows0, ng * kRows0, f.CB, &fin, nth);
 }
 
 template <int ELEM, int MODE, bool XBF16, bool PIPE, int NR, int PEEK = kPeek>
 __global__ void __launch_bounds__(1024) k_layout0(BlockArgs a) {
-    layout0_body<ELEM, MODE, XBF16, PIPE, NR, PEEK>(a, blockDim.x, kFinishAll);
+    __shared__ LutT<PEEK> s;
+    extern __shared__ uint32_t dyn[];
+    layout0_body<ELEM, MODE, XBF16, PIPE, NR, PEEK>(a, blockDim.x, kFinishAll, blockIdx.x * a.G, 0u, s, dyn);
 }
 
 // The single-round token kernel (BF16 x, 13-bit table) with the inputs of its first requests as leading scalar
@@ -527,9 +534,44 @@ __global__ void __launch_bounds__(1024) k_layout0p(const uint32_t *__restrict__ 
                                                    const uint8_t *__restrict__ hdr, const void *__restrict__ xp,
                                                    uint32_t M, uint32_t K, uint32_t pk, const uint16_t *__restrict__ aux,
                                                    BlockArgs a) {
+    __shared__ LutT<kPeekSeq> s;
+    extern __shared__ uint32_t dyn[];
     a.bases = bases; a.seq = seq; a.hdr = hdr; a.x = xp; a.M = M; a.K = K; a.aux = aux;
     a.G = pk & 0xFFFFu;
-    layout0_body<ELEM, kToken, true, false, NR, kPeekSeq>(a, ((pk >> 16) & 0x3FFFu) * 32u, pk >> 30);
+    layout0_body<ELEM, kToken, true, false, NR, kPeekSeq>(a, ((pk >> 16) & 0x3FFFu) * 32u, pk >> 30, blockIdx.x * a.G, 0u,
+                                                          s, dyn);
+}
+
+// Layout-0 token path for matrices of one to two row groups per CU (k_layout0t): the first nfull workgroups (one per
+// CU) take a whole row group each (NRF rows per half-wave, as k_layout0p); the TS-way parts (rows 8 / TS each, from
+// the row index) of the remaining row groups go one to a workgroup, so every CU decodes about the same rows instead
+// of some CUs two whole row groups (Qwen3-4B down and o_proj: 320 row groups on 256 CUs).  A part's workgroup stages
+// its row group's streams whole, so those streams are read TS times (from L2 / the MALL after the first).
+// pk = nfull | H << 16 | has_scale << 30 | has_bias << 31.
+template <int ELEM, int NRF, int TS>
+__global__ void __launch_bounds__(1024) k_layout0t(const uint32_t *__restrict__ bases, const uint32_t *__restrict__ seq,
+                                                   const uint8_t *__restrict__ hdr, const void *__restrict__ xp,
+                                                   uint32_t M, uint32_t K, uint32_t pk, const uint16_t *__restrict__ aux,
+                                                   BlockArgs a) {
+    static_assert(TS == 2 || TS == 4, "halves or quarters of a row group");
+    __shared__ LutT<kPeekSeq> s;
+    extern __shared__ uint32_t dyn[];
+    a.bases = bases; a.seq = seq; a.hdr = hdr; a.x = xp; a.M = M; a.K = K; a.aux = aux;
+    a.G = 1;
+    const uint32_t nfull = pk & 0xFFFFu, nth = ((pk >> 16) & 0x3FFFu) * 32u, flags = pk >> 30;
+    if (blockIdx.x < nfull) {
+        layout0_body<ELEM, kToken, true, false, NRF, kPeekSeq>(a, nth, flags, blockIdx.x, 0u, s, dyn);
+    } else {
+        const uint32_t q = blockIdx.x - nfull;
+        layout0_body<ELEM, kToken, true, false, 8 / TS, kPeekSeq, true>(a, nth, flags, nfull + q / TS, q % TS, s, dyn);
+    }
+}
+
+template <int ELEM, int NRF, int TS>
+static void launch_layout0t(const LaunchPlan &p, const BlockArgs &a, hipStream_t st) {
+    const uint32_t pk = p.G | ((p.threads / 32u) << 16) | (a.scale ? 1u << 30 : 0u) | (a.bias ? 1u << 31 : 0u);
+    hipLaunchKernelGGL((k_layout0t<ELEM, NRF, TS>), dim3(p.grid), dim3(p.threads), p.lds, st, a.bases, a.seq, a.hdr, a.x,
+                       a.M, a.K, pk, a.aux, a);
 }
 
 template <int ELEM, int NR>
@@ -1200,6 +1242,19 @@ static int launch_prefix_t(const LaunchPlan &p, const BlockArgs &a, hipStream_t 
         return (int)hipGetLastError();
     }
     if constexpr (MODE == kToken && XBF16) {
+        if (p.layout == 0 && p.tail) {                         // whole row groups + split tail (k_layout0t)
+            const uint32_t nrf = 8u / p.split;
+            if (p.tail == 4) {
+                if (nrf == 2) launch_layout0t<ELEM, 2, 4>(p, a, st);
+                else if (nrf == 4) launch_layout0t<ELEM, 4, 4>(p, a, st);
+                else launch_layout0t<ELEM, 8, 4>(p, a, st);
+            } else {
+                if (nrf == 2) launch_layout0t<ELEM, 2, 2>(p, a, st);
+                else if (nrf == 4) launch_layout0t<ELEM, 4, 2>(p, a, st);
+                else launch_layout0t<ELEM, 8, 2>(p, a, st);
+            }
+            return (int)hipGetLastError();
+        }
         if (p.layout == 0 && p.seq13 && !p.pipe && p.G < 65536u) {
             if (p.split == 2) launch_layout0p<ELEM, 4>(p, a, st);
             else if (p.split == 4) launch_layout0p<ELEM, 2>(p, a, st);

@@ -10,6 +10,7 @@ struct LaunchPlan {
     uint32_t split;         // layout 0: half-waves per block (1, or 2 or 4 with the row index)
     bool seq13;             // layout 0 token path: the 13-bit decode table (a larger static LDS share)
     bool multi;             // layout 1: several items (block, quarter) per half-wave, one 16-row group per workgroup
+    uint32_t tail;          // layout 0 token path: k_layout0t, G whole row groups then the rest split tail-ways (2, 4)
     uint32_t grid, threads, lds, G;
     uint32_t slot_words;    // layout 0: region-buffer words per block
 };

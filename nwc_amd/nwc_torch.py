@@ -351,7 +351,8 @@ class NWCWeight:
     def token_bytes(self):
         """Bytes one token-path call reads: the compressed matrix, the row-index entries its plan uses (64 per block
         at two half-waves per block, 192 at four) and the 13-bit table."""
-        split = lib.nwc_token_split(self.n, self.in_features, self.code, int(self.row_index() is not None))
+        flags = int(self.row_index() is not None) | int(self.seq_table() is not None) << 1
+        split = lib.nwc_token_split(self.n, self.in_features, self.code, flags)
         table = 4 * SEQ_TABLE_WORDS if self.seq_table() is not None else 0
         return self.bytes + self.bases.numel() * LANES * 2 * (split - 1) + table
 

@@ -285,6 +285,48 @@ def test_token_path_with_and_without_row_index(cuda, layout, M, K, split, escape
         check_rne(y, y64, token_tol(y64))
 
 
+@pytest.mark.parametrize("M,K,elem,escapes", [
+    (2560, 4096, "bf16", "none"), (2560, 9728, "bf16", "dense"), (2560, 9728, "fp8", "none"), (2560, 1000, "bf16", "sparse"),
+    (2880, 2048, "bf16", "none"), (2880, 9728, "bf16", "heavy"), (2600, 4096, "fp8", "dense"), (2050, 512, "bf16", "none")])
+def test_split_tail_plan(cuda, M, K, elem, escapes):
+    """Matrices of one to two row groups per CU take k_layout0t (one whole row group per CU, the rest cut into
+    quarters or halves of their rows): results bit-identical to the whole-block decode without the row index (every
+    row's lanes and column blocks are summed in one order), and rounded from within 1e-3 of float64, with scale and
+    bias; shapes with 320 row groups (quarters), 360 (halves), ragged K, escapes that overflow the staged region, and
+    fp8."""
+    from nwc_amd._abi import lib as _lib, ptr as _ptr, stream as _stream
+    NWCWeight, _, quantize_fp8 = _nwc()
+    print(f"tail plan {M}x{K} {elem} {escapes}", flush=True)
+    w = bf16_matrix(M, K, seed=M + K + 3, escapes=escapes == "sparse")
+    if escapes == "dense":
+        big = torch.tensor(1e30, dtype=torch.bfloat16)
+        w[M - 20:M - 12, 0:64] = big
+        w[M - 7, 512:700] = -big
+    if escapes == "heavy":                    # the last 24 rows all escapes: the tail's streams exceed their region
+        sign = torch.randint(0, 2, (24, K), generator=torch.Generator().manual_seed(5)) * 2 - 1
+        w[M - 24:M] = (sign * 1e30).to(torch.bfloat16)
+    c = NWCWeight(w, device="cuda", layout=0, elem=elem)
+    assert _lib.nwc_token_split(c.n, K, c.code, 3) >= 1
+    g = torch.Generator().manual_seed(8)
+    x = torch.randn(K, generator=g).to(torch.bfloat16).cuda()
+    bias = (torch.rand(M, generator=g) - 0.5).to(torch.bfloat16).cuda()
+    xin = c._padded(x).contiguous()
+    ys = []
+    for ri in (c.row_index(), None):
+        y = torch.empty(M, dtype=torch.bfloat16, device="cuda")
+        assert _lib.nwc_linear_xbf16(_stream(), _ptr(c.data), _ptr(c.bases), _ptr(c.hdr), _ptr(c.lut), _ptr(c.low),
+                                     _ptr(ri) if ri is not None else None, _ptr(c.seq_table()), _ptr(xin), _ptr(bias),
+                                     _ptr(c.scale), _ptr(y), c.n, K, c.code) == 0
+        ys.append(y.cpu())
+    assert torch.equal(ys[0].view(torch.int16), ys[1].view(torch.int16))
+    wd = c.dequant().double()
+    if c.scale is not None:
+        wd = wd * c.scale.double()[:, None]
+    y64 = (wd @ x.double() + bias.double()).cpu().numpy()
+    terms = (wd.abs() @ x.double().abs()).cpu().numpy()
+    check_rne(ys[0], y64, token_tol(y64, terms))
+
+
 @pytest.mark.parametrize("M,K,escapes", [(4608, 3584, "none"), (3584, 3584, "dense"), (1003, 1100, "dense"),
                                           (16, 512, "none"), (2000, 3000, "dense"), (37888, 3584, "dense"),
                                           (3584, 18944, "none"), (1000, 17000, "dense")])
