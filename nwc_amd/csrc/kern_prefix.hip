@@ -182,7 +182,7 @@ __device__ __forceinline__ float row0(Seq<ELEM, STRIDE> &S, const Tab &s, const 
         const uint32_t s0 = S.s;
         const uint32_t *wp0 = S.wp;
         uint32_t e1, e2;
-        if (__any(S.fast_quad(s, e1, e2) >= kSeqSlowTest)) {
+        if (__builtin_expect(__any(S.fast_quad(s, e1, e2) >= kSeqSlowTest), 0)) {
             S.s = s0;
             S.wp = wp0;
             S.reload();
@@ -211,7 +211,7 @@ __device__ __forceinline__ void row_codes(Seq<ELEM> &S, const Tab &s, uint32_t (
     for (int k = 0; k < 4; k++) {
         const uint32_t s0 = S.s;
         const uint32_t *wp0 = S.wp;
-        if (__any(S.fast_quad(s, e1[k], e2[k]) >= kSeqSlowTest)) {
+        if (__builtin_expect(__any(S.fast_quad(s, e1[k], e2[k]) >= kSeqSlowTest), 0)) {
             S.s = s0;
             S.wp = wp0;
             S.reload();
@@ -769,7 +769,7 @@ __device__ __forceinline__ float2 chunks1(const Tab &s, const uint32_t *lane, ui
             const uint32_t s0 = S.s;
             const uint32_t *wp0 = S.wp;
             uint32_t e1, e2;
-            if (__any(S.fast_quad(s, e1, e2) >= kSeqSlowTest)) {
+            if (__builtin_expect(__any(S.fast_quad(s, e1, e2) >= kSeqSlowTest), 0)) {
                 S.s = s0;
                 S.wp = wp0;
                 S.reload();
@@ -830,7 +830,7 @@ __device__ __forceinline__ float2 chunks1_global(const Tab &s, const uint32_t *l
             const uint32_t s0 = S.s;
             const uint32_t *wp0 = S.wp;
             uint32_t e1, e2;
-            if (__any(S.fast_quad(s, e1, e2) >= kSeqSlowTest)) {
+            if (__builtin_expect(__any(S.fast_quad(s, e1, e2) >= kSeqSlowTest), 0)) {
                 S.s = s0;
                 S.wp = wp0;
                 S.reload();
@@ -1305,7 +1305,7 @@ __device__ __forceinline__ void row0_batch(Seq<ELEM> &S, const Tab &s, const uin
         const uint32_t s0 = S.s;
         const uint32_t *wp0 = S.wp;
         uint32_t e1, e2;
-        if (__any(S.fast_quad(s, e1, e2) >= kSeqSlowTest)) {
+        if (__builtin_expect(__any(S.fast_quad(s, e1, e2) >= kSeqSlowTest), 0)) {
             S.s = s0;
             S.wp = wp0;
             S.reload();
@@ -1551,7 +1551,7 @@ __global__ void __launch_bounds__(256) k_gather1x(GatherArgs a, const uint16_t *
             const uint32_t s0 = S.s;
             const uint32_t *wp0 = S.wp;
             uint32_t e1, e2;
-            if (__any(S.fast_quad(s, e1, e2) >= kSeqSlowTest)) {
+            if (__builtin_expect(__any(S.fast_quad(s, e1, e2) >= kSeqSlowTest), 0)) {
                 S.s = s0;
                 S.wp = wp0;
                 S.reload();

@@ -385,23 +385,18 @@ struct Seq {
     template <int PEEK>
     __device__ __forceinline__ uint32_t slow_code(const LutT<PEEK> &T) {
         const uint32_t hi = window() << 1;                             // the bits from P (codes take at most 24)
-        uint32_t u = __clz((int)hi), b, c;
-        if (ELEM == kElemFp8 || u < kMaxRankBf16) {
-            u = u < 15u ? u : 15u;
-            b = (((hi >> (30u - u)) & 1u) << 7) | T.eor[u];
-            c = u + 2u;
-        } else {
-            b = (hi >> 8) & 0xFFu;
-            c = 24u;
-        }
-        step((s & 31u) - c);
+        const uint32_t u = min((uint32_t)__clz((int)hi), 15u);
+        const bool esc = ELEM != kElemFp8 && u >= kMaxRankBf16;       // BF16: 15 zeros, one, the byte
+        const uint32_t br = (((hi >> (30u - u)) & 1u) << 7) | T.eor[u];
+        const uint32_t b = esc ? (hi >> 8) & 0xFFu : br;             // no branch: the wave stays converged
+        step((s & 31u) - (esc ? 24u : u + 2u));
         return b;
     }
     template <int PEEK>
     __device__ __forceinline__ void slow_quad(const LutT<PEEK> &T, uint32_t &e1, uint32_t &e2) {
-        uint32_t bytes = slow_code(T) << 24;                           // b3 b2 b1 b0 after four codes
+        uint32_t bytes = 0;                                            // b3 b2 b1 b0 after four codes
 #pragma unroll 1
-        for (int k = 1; k < 4; k++) bytes = (bytes >> 8) | (slow_code(T) << 24);
+        for (int k = 0; k < 4; k++) bytes = (bytes >> 8) | (slow_code(T) << 24);
         e1 = (bytes << 8) & 0x00FFFF00u;
         e2 = (bytes >> 8) & 0x00FFFF00u;
     }
