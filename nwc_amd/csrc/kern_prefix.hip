@@ -201,6 +201,12 @@ __device__ __forceinline__ float row0(Seq<ELEM, STRIDE> &S, const Tab &s, const 
 // arrived, so decoding starts sooner (a deeper ring, or rows requested together with the streams, measured slower:
 // the whole chip's first requests compete for HBM, and the workgroup waits for all of its streams).
 constexpr int kRing0 = 2;
+// Dequantization requests all of a half-wave's raw rows at once: its row stores share the in-order vector-memory
+// counter with the raw loads, so a wait for raw row r also waits for every store requested before row r's load (4B
+// dequantization per stack, ring of 2 / 4 / 8 rows: 3072 / 3047 / 2929 us; gate_up 38.8 / 37.8 / 35.2 us).
+constexpr int kRingD = 8;
+template <int MODE>
+constexpr int ring_depth() { return MODE == kDequant ? kRingD : kRing0; }
 
 // The table entries of one row's 16 weights for one lane (four steps of the cursor; a step that was not fast in some
 // lane is redone code by code by the whole wave), kept apart from their use so that a row can be decoded before its
@@ -241,7 +247,8 @@ __device__ __forceinline__ float row_dot(const uint32_t (&e1)[4], const uint32_t
 // time to arrive (Qwen3-4B sweep 1726 -> 1695 us per token; two rows behind measured slower, 1743 us).
 template <int ELEM, int MODE, bool XBF16, int NR, class Tab>
 __device__ __forceinline__ float rowsN(const Tab &s, const uint32_t *lane, uint32_t P0, const BlockArgs &a, const Shape &f,
-                                       const XRegs<XBF16> &x, uint4 ring[kRing0], const Coord0 &c, uint32_t r0, uint32_t L) {
+                                       const XRegs<XBF16> &x, uint4 *ring, const Coord0 &c, uint32_t r0, uint32_t L) {
+    constexpr int RING = ring_depth<MODE>();
     Seq<ELEM> S;
     S.init_at(lane, P0);
     float acc[NR];
@@ -264,9 +271,9 @@ __device__ __forceinline__ float rowsN(const Tab &s, const uint32_t *lane, uint3
         if (MODE == kRowIndex && r > 0 && (r & 1) == 0)
             ((uint16_t *)a.out)[((uint64_t)c.b * kRowIndexSplits + (r >> 1) - 1) * kLanes + L] = (uint16_t)S.position(lane);
         uint32_t pw[8];
-        const float sum = row0<ELEM, MODE, XBF16>(S, s, ring[r % kRing0], x, pw);
-        // eight rows go through a ring of kRing0 registers: row r + kRing0 is requested when row r is done
-        if (MODE != kRowIndex && r + kRing0 < NR) ring[r % kRing0] = raw_row<ELEM>(a.low, f, c, r + kRing0);
+        const float sum = row0<ELEM, MODE, XBF16>(S, s, ring[r % RING], x, pw);
+        // eight rows go through a ring of RING registers: row r + RING is requested when row r is done
+        if (MODE != kRowIndex && r + RING < NR) ring[r % RING] = raw_row<ELEM>(a.low, f, c, r + RING);
         if (MODE == kDequant) store_row0<MODE>(a, f, c.row0 + r0 + r, c.col0, c.col_ok, pw);
         else acc[r] = c.col_ok ? sum : 0.f;
     }
@@ -400,7 +407,8 @@ __device__ __forceinline__ void layout0_body(BlockArgs a, uint32_t nth, uint32_t
                                              LutT<PEEK> &s, uint32_t *dyn) {
     static_assert(NR == 8 || ((NR == 4 || NR == 2) && !PIPE), "row splits only in the single-round kernel");
     static_assert(PEEK == kPeek || !PIPE, "the 13-bit table only in the single-round kernel");
-    static_assert(!PART || (NR < 8 && !PIPE && MODE == kToken), "a row part of a single row group, token path");
+    static_assert(!PART || (NR < 8 && !PIPE && (MODE == kToken || MODE == kDequant)),
+                  "a row part of a single row group, token path or dequantization");
     constexpr uint32_t SP = PART ? 1u : kRows0 / NR;         // half-waves per block
     constexpr bool ROWS = MODE == kToken || MODE == kF32;     // modes that keep row sums
     const uint32_t tid = threadIdx.x, L = tid & 31;
@@ -449,10 +457,11 @@ __device__ __forceinline__ void layout0_body(BlockArgs a, uint32_t nth, uint32_t
         Q.finish(s, a, nth);
         const bool fits = R.n16 * 4u <= cap;
         if (fits) bulk_commit(Bk, cur, R, tid, nth);
-        uint4 raw[kRing0];
+        constexpr int RING = ring_depth<MODE>();
+        uint4 raw[RING];
         __syncthreads();
 #pragma unroll
-        for (int r = 0; r < (NR < kRing0 ? NR : kRing0); r++)
+        for (int r = 0; r < (NR < RING ? NR : RING); r++)
             raw[r] = MODE == kRowIndex ? make_uint4(0u, 0u, 0u, 0u) : raw_row<ELEM>(a.low, f, c, r);
         if (t < nt) {
             const uint32_t start = c.col_ok ? half_scan_incl(n, L) - n : 0u;
@@ -513,7 +522,7 @@ __device__ __forceinline__ void layout0_body(BlockArgs a, uint32_t nth, uint32_t
             t += H;
         }
     }
-    if (PART) finish_rows<MODE>(a, part + r0 * f.CB, rg0 * kRows0 + r0, NR, f.CB, &fin, nth);
+    if (PART && ROWS) finish_rows<MODE>(a, part + r0 * f.CB, rg0 * kRows0 + r0, NR, f.CB, &fin, nth);
     else if (ROWS) finish_rows<MODE>(a, part, rg0 * kRows0, ng * kRows0, f.CB, &fin, nth);
 }
 
@@ -542,36 +551,53 @@ __global__ void __launch_bounds__(1024) k_layout0p(const uint32_t *__restrict__ 
                                                           s, dyn);
 }
 
-// Layout-0 token path for matrices of one to two row groups per CU (k_layout0t): the first nfull workgroups (one per
-// CU) take a whole row group each (NRF rows per half-wave, as k_layout0p); the TS-way parts (rows 8 / TS each, from
-// the row index) of the remaining row groups go one to a workgroup, so every CU decodes about the same rows instead
-// of some CUs two whole row groups (Qwen3-4B down and o_proj: 320 row groups on 256 CUs).  A part's workgroup stages
-// its row group's streams whole, so those streams are read TS times (from L2 / the MALL after the first).
-// pk = nfull | H << 16 | has_scale << 30 | has_bias << 31.
-template <int ELEM, int NRF, int TS>
+// Layout-0 token path and dequantization for matrices of one to two row groups per CU (k_layout0t): the first nfull
+// workgroups (one per CU) take a whole row group each (NRF rows per half-wave, as k_layout0p); the TS-way parts (rows
+// 8 / TS each, from the row index) of the remaining row groups go one to a workgroup, so every CU decodes about the
+// same rows instead of some CUs two whole row groups (Qwen3-4B down and o_proj: 320 row groups on 256 CUs).  A part's
+// workgroup stages its row group's streams whole, so those streams are read TS times (from L2 / the MALL after the
+// first).  pk = nfull | H << 16 | has_scale << 30 | has_bias << 31 (scale and bias: token path only).
+template <int ELEM, int NRF, int TS, int MODE = kToken>
 __global__ void __launch_bounds__(1024) k_layout0t(const uint32_t *__restrict__ bases, const uint32_t *__restrict__ seq,
                                                    const uint8_t *__restrict__ hdr, const void *__restrict__ xp,
                                                    uint32_t M, uint32_t K, uint32_t pk, const uint16_t *__restrict__ aux,
                                                    BlockArgs a) {
     static_assert(TS == 2 || TS == 4, "halves or quarters of a row group");
+    static_assert(MODE == kToken || MODE == kDequant, "token path or dequantization");
     __shared__ LutT<kPeekSeq> s;
     extern __shared__ uint32_t dyn[];
     a.bases = bases; a.seq = seq; a.hdr = hdr; a.x = xp; a.M = M; a.K = K; a.aux = aux;
     a.G = 1;
     const uint32_t nfull = pk & 0xFFFFu, nth = ((pk >> 16) & 0x3FFFu) * 32u, flags = pk >> 30;
     if (blockIdx.x < nfull) {
-        layout0_body<ELEM, kToken, true, false, NRF, kPeekSeq>(a, nth, flags, blockIdx.x, 0u, s, dyn);
+        layout0_body<ELEM, MODE, true, false, NRF, kPeekSeq>(a, nth, flags, blockIdx.x, 0u, s, dyn);
     } else {
         const uint32_t q = blockIdx.x - nfull;
-        layout0_body<ELEM, kToken, true, false, 8 / TS, kPeekSeq, true>(a, nth, flags, nfull + q / TS, q % TS, s, dyn);
+        layout0_body<ELEM, MODE, true, false, 8 / TS, kPeekSeq, true>(a, nth, flags, nfull + q / TS, q % TS, s, dyn);
     }
 }
 
-template <int ELEM, int NRF, int TS>
+template <int ELEM, int NRF, int TS, int MODE>
 static void launch_layout0t(const LaunchPlan &p, const BlockArgs &a, hipStream_t st) {
     const uint32_t pk = p.G | ((p.threads / 32u) << 16) | (a.scale ? 1u << 30 : 0u) | (a.bias ? 1u << 31 : 0u);
-    hipLaunchKernelGGL((k_layout0t<ELEM, NRF, TS>), dim3(p.grid), dim3(p.threads), p.lds, st, a.bases, a.seq, a.hdr, a.x,
-                       a.M, a.K, pk, a.aux, a);
+    hipLaunchKernelGGL((k_layout0t<ELEM, NRF, TS, MODE>), dim3(p.grid), dim3(p.threads), p.lds, st, a.bases, a.seq,
+                       a.hdr, a.x, a.M, a.K, pk, a.aux, a);
+}
+
+// the split-tail plan's kernel by rows per half-wave of a whole row group (8 / split) and parts per row group
+template <int ELEM, int MODE>
+static int launch_layout0_tail(const LaunchPlan &p, const BlockArgs &a, hipStream_t st) {
+    const uint32_t nrf = 8u / p.split;
+    if (p.tail == 4) {
+        if (nrf == 2) launch_layout0t<ELEM, 2, 4, MODE>(p, a, st);
+        else if (nrf == 4) launch_layout0t<ELEM, 4, 4, MODE>(p, a, st);
+        else launch_layout0t<ELEM, 8, 4, MODE>(p, a, st);
+    } else {
+        if (nrf == 2) launch_layout0t<ELEM, 2, 2, MODE>(p, a, st);
+        else if (nrf == 4) launch_layout0t<ELEM, 4, 2, MODE>(p, a, st);
+        else launch_layout0t<ELEM, 8, 2, MODE>(p, a, st);
+    }
+    return (int)hipGetLastError();
 }
 
 template <int ELEM, int NR>
@@ -1241,20 +1267,10 @@ static int launch_prefix_t(const LaunchPlan &p, const BlockArgs &a, hipStream_t 
         hipLaunchKernelGGL((k_layout0<ELEM, MODE, XBF16, true, 8>), dim3(p.grid), dim3(p.threads), p.lds, st, a);
         return (int)hipGetLastError();
     }
+    if constexpr ((MODE == kToken && XBF16) || MODE == kDequant) {
+        if (p.layout == 0 && p.tail) return launch_layout0_tail<ELEM, MODE>(p, a, st);   // whole row groups + split tail
+    }
     if constexpr (MODE == kToken && XBF16) {
-        if (p.layout == 0 && p.tail) {                         // whole row groups + split tail (k_layout0t)
-            const uint32_t nrf = 8u / p.split;
-            if (p.tail == 4) {
-                if (nrf == 2) launch_layout0t<ELEM, 2, 4>(p, a, st);
-                else if (nrf == 4) launch_layout0t<ELEM, 4, 4>(p, a, st);
-                else launch_layout0t<ELEM, 8, 4>(p, a, st);
-            } else {
-                if (nrf == 2) launch_layout0t<ELEM, 2, 2>(p, a, st);
-                else if (nrf == 4) launch_layout0t<ELEM, 4, 2>(p, a, st);
-                else launch_layout0t<ELEM, 8, 2>(p, a, st);
-            }
-            return (int)hipGetLastError();
-        }
         if (p.layout == 0 && p.seq13 && !p.pipe && p.G < 65536u) {
             if (p.split == 2) launch_layout0p<ELEM, 4>(p, a, st);
             else if (p.split == 4) launch_layout0p<ELEM, 2>(p, a, st);

@@ -293,7 +293,7 @@ def test_split_tail_plan(cuda, M, K, elem, escapes):
     quarters or halves of their rows): results bit-identical to the whole-block decode without the row index (every
     row's lanes and column blocks are summed in one order), and rounded from within 1e-3 of float64, with scale and
     bias; shapes with 320 row groups (quarters), 360 (halves), ragged K, escapes that overflow the staged region, and
-    fp8."""
+    fp8.  Dequantization takes the same plan: the original bits, equal to the whole-block kernel's."""
     from nwc_amd._abi import lib as _lib, ptr as _ptr, stream as _stream
     NWCWeight, _, quantize_fp8 = _nwc()
     print(f"tail plan {M}x{K} {elem} {escapes}", flush=True)
@@ -319,7 +319,16 @@ def test_split_tail_plan(cuda, M, K, elem, escapes):
                                      _ptr(c.scale), _ptr(y), c.n, K, c.code) == 0
         ys.append(y.cpu())
     assert torch.equal(ys[0].view(torch.int16), ys[1].view(torch.int16))
-    wd = c.dequant().double()
+    # dequantization through the same plan (nwc_dequant_seq) against the whole-block kernel without the row index
+    # (nwc_dequant) and, for BF16, against the encoded bits
+    plain = torch.empty(M, c.K16, dtype=torch.bfloat16, device="cuda")
+    assert _lib.nwc_dequant(_stream(), _ptr(c.data), _ptr(c.bases), _ptr(c.hdr), _ptr(c.lut), _ptr(c.low), _ptr(plain),
+                            c.n, c.block, K, c.code) == 0
+    got = c.dequant()
+    assert torch.equal(got.cpu().view(torch.int16), plain[:, :K].cpu().view(torch.int16))
+    if elem == "bf16":
+        assert torch.equal(got.cpu().view(torch.int16), w.view(torch.int16))
+    wd = got.double()
     if c.scale is not None:
         wd = wd * c.scale.double()[:, None]
     y64 = (wd @ x.double() + bias.double()).cpu().numpy()
