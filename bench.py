@@ -140,7 +140,7 @@ def avg_launch_ms(fn, rotate, replays):
     return e0.elapsed_time(e1) / (rotate * replays)
 
 
-DOMINANT = "gate_up"            # the roofline's kernel: the largest matrix (k_layout0, single round, 8 rows, 13-bit table)
+DOMINANT = "gate_up"            # the roofline's kernel: the largest matrix (k_layout0p<BF16, 8 rows>: one round, 13-bit table)
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_gate_up.json")
 
 
@@ -1174,7 +1174,7 @@ def main():
         "speedup_vs_native_fp8": None if g["fp8"] is None else round(g["fp8"]["us_per_token_graph"] / us_tok, 3),
         "roofline": {"bound": "hbm", "achieved": round(g["achieved"], 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(g["achieved"] / PEAK_HBM_GBS, 4), "traffic": traffic_bytes() if args.config == "qwen3-4b" and layout == 0 else None,
-                     "kernel": f"{'k_layout0<BF16, token, BF16 x, single round, 8 rows, 13-bit table>' if layout == 0 else f'layout {layout} kernel'}"
+                     "kernel": f"{'k_layout0p<BF16, 8 rows> (token path, BF16 x, one round, 13-bit table, preloaded arguments)' if layout == 0 else f'layout {layout} kernel'}"
                                f": gate_up {dict((n, (M, K)) for n, M, K in shapes)['gate_up']}",
                      "bytes_per_launch": g["dom_bytes"], "avg_launch_us": round(g["dom_us"], 2),
                      "achieved_basis": "NWCWeight.bytes (+ row-index entries read) + x + y of one gate_up launch / "
