@@ -48,7 +48,7 @@ def test_info():
 
 
 @pytest.mark.parametrize("M,K,elem,expect", [
-    (19456, 2560, 0x00, (12160, 19456 * 2560, 19456 * 5, 2560)),      # nb, raw bytes, scratch, K16
+    (19456, 2560, 0x00, (12160, 19456 * 2560, 19456 * 5, 2560)),      # Qwen3-4B gate_up: nb, raw bytes, scratch, K16
     (2560, 9728, 0x00, (6080, 2560 * 9728, 2560 * 19, 9728)),
     (13, 40, 0x00, (2, 13 * 48, 16, 48)),                              # M * K16 raw bytes, Mp * CB
 ])
