@@ -8,6 +8,14 @@
  * buffer belong to the caller.  `elem` = element type (0 BF16, 1 fp8 e4m3fn) | layout << 4 (layouts 0, 1, 2).
  * `block` must be 4096 (nwc_info(4)); K is the number of columns, n = M * K.
  *
+ * This build's extension of `elem` (no counterpart in the reference, whose callers leave these bits zero): bits
+ * 8-15 = S / 16 for a layout-0 matrix whose block streams sit in fixed slots of S bytes (16 <= S <= 1728, a
+ * multiple of 16): block b's lane streams start at byte b * S of `data`, bases[b] == b * S, and `data` holds
+ * nb * S + 128 bytes (the slots' padding and the tail zero).  Such tensors are still a valid tensor set of the
+ * format; the bits only let the token kernels compute a block's offset instead of reading bases[b] before they can
+ * request its streams.  A caller that sets them for tensors that do not meet this contract makes the kernels read
+ * the wrong bytes.  The bits are refused (-1) for layouts 1/2, for S > 1728, or when nb * S + 128 >= 2^32.
+ *
  * Device entry points return 0, -1 for a shape the format cannot describe (or, in this build, a raw plane the
  * kernels cannot address with 32-bit offsets: layout 0 with Mp * K16 >= 2^32 for Mp = M rounded up to 8 rows,
  * layouts 1/2 with a plane of 2^32 - 512 bytes or more), or a hipError_t code of the launch.  `low` must be followed by the format's 512

@@ -37,14 +37,17 @@ int current_cus() {
 // This build also addresses the raw planes with 32-bit offsets: layout 0 counts weights of the padded matrix
 // (Mp * K16, rows past M included), layouts 1/2 count bytes of the plane padded to 16 rows and 32 columns plus its
 // 512 slack bytes; both must stay below 2^32.
+// Bits 8-15 of elem (a fixed-slot stride, layout 0 only) are this build's; the reference's callers leave them zero.
 bool shape_ok(uint64_t n, uint32_t block, uint32_t K, int elem) {
     if (!(block == kBlock && K != 0 && n % K == 0 && n / K >= 1 && n / K <= 0xFFFFFFFFull && elem_type(elem) <= 1 &&
-          elem_layout(elem) <= 2 && (elem & ~0xFF) == 0))
+          elem_layout(elem) <= 2 && (elem & ~0xFFFF) == 0 && (elem_layout(elem) == 0 || elem_stride(elem) == 0) &&
+          elem_stride(elem) <= kSlotMax))
         return false;
     const uint64_t M = n / K, K16 = (K + 15u) & ~15u;
     if (M * K16 >= (1ull << 32)) return false;          // also keeps Shape's 32-bit fields (M < 2^28) from wrapping
     const Shape f((uint32_t)M, K, elem_layout(elem));
-    if (elem_layout(elem) == 0) return (uint64_t)f.Mp * f.K16 < (1ull << 32);
+    if (elem_layout(elem) == 0)
+        return (uint64_t)f.Mp * f.K16 < (1ull << 32) && (uint64_t)f.nb * elem_stride(elem) + 128u < (1ull << 32);
     return f.low_bytes(elem) + kRawSlack < (1ull << 32);
 }
 
@@ -391,7 +394,7 @@ int run_blocks(int mode, bool xbf16, hipStream_t st, const uint8_t *data, const 
                      t == kElemFp8))
         return -1;
     BlockArgs a{data, bases, hdr, tab, low, x, bias, scale, out, aux, f.M, f.K, p.G,
-                layout == 0 || p.split ? p.slot_words : slot_words_for(layout), seq};
+                layout == 0 || p.split ? p.slot_words : slot_words_for(layout), seq, elem_stride(elem)};
     return layout == 2 ? launch_fixed(p, t, mode, xbf16, a, st) : launch_prefix(p, t, mode, xbf16, a, st);
 }
 
@@ -463,7 +466,8 @@ extern "C" int nwc_linear_xbf16_batch(void *stream, const uint8_t *data, const u
     const Shape f((uint32_t)(n / K), K, 0);
     LaunchPlan p;
     if (!plan_layout0_batch(f, ncu, ntok, seq_table != nullptr, p)) return -1;
-    BlockArgs a{data, bases, hdr, tab, low, x, bias, scale, y, nullptr, f.M, f.K, p.G, p.slot_words, seq_table};
+    BlockArgs a{data, bases, hdr, tab, low, x, bias, scale, y, nullptr, f.M, f.K, p.G, p.slot_words, seq_table,
+                elem_stride(elem)};
     return launch_layout0_batch(p, elem_type(elem), a, ntok, (hipStream_t)stream);
 }
 
@@ -487,7 +491,8 @@ extern "C" int nwc_prefill_xbf16(void *stream, const uint8_t *data, const uint32
     if (ncu <= 0) return (int)hipErrorNoDevice;
     const Shape f((uint32_t)(n / K), K, 0);
     const uint32_t row_tiles = (f.groups() + 7u) / 8u;
-    PrefillArgs p{BlockArgs{data, bases, hdr, tab, low, nullptr, bias, scale, y, row_index, f.M, f.K, 8u, 0u, seq_table},
+    PrefillArgs p{BlockArgs{data, bases, hdr, tab, low, nullptr, bias, scale, y, row_index, f.M, f.K, 8u, 0u, seq_table,
+                            elem_stride(elem)},
                   x, ntok};
     return launch_prefill0(elem_type(elem), prefill_tokens_per_tile(row_tiles, ntok, ncu), p, (hipStream_t)stream);
 }

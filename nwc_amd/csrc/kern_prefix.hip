@@ -125,6 +125,7 @@ __device__ __forceinline__ void store_row0(const BlockArgs &a, const Shape &f, u
 // The blocks of a workgroup's tile are consecutive in `data`, so a round of H blocks (one per half-wave) is one
 // contiguous byte range: [bases[b_lo], bases[b_hi]) -- for the matrix's last block, its base plus four bytes per header
 // word.  All threads copy it into LDS with 16-byte loads; no half-wave needs its own header scan before the copy.
+// With fixed slots (stride != 0) the range is [b_lo * stride, b_hi * stride) and nothing is read to find it.
 struct Region {
     uint32_t lo16, n16;         // 16-byte aligned start (byte offset into data), 16-byte chunks
 };
@@ -139,10 +140,16 @@ __device__ __forceinline__ uint32_t matrix_end(const BlockArgs &a, uint32_t nb) 
 }
 
 // Blocks [b_lo, b_hi) plus the 16 bytes the last lane's window reads past its stream (inside the 64 slack bytes that
-// follow the matrix's last block).
-__device__ __forceinline__ Region region_of(const BlockArgs &a, uint32_t b_lo, uint32_t b_hi, uint32_t nb, uint32_t mend) {
-    const uint32_t s = a.bases[b_lo], e = a.bases[min(b_hi, nb - 1u)];
+// follow the matrix's last block, or the 128 after its last slot).  stride: a.stride for layout 0, 0 for layout 1.
+__device__ __forceinline__ Region region_of(const BlockArgs &a, uint32_t b_lo, uint32_t b_hi, uint32_t nb, uint32_t mend,
+                                            uint32_t stride) {
     Region r;
+    if (stride) {
+        r.lo16 = b_lo * stride;                                 // a multiple of 16
+        r.n16 = ((b_hi > b_lo ? b_hi - b_lo : 0u) * stride + 31u) >> 4;
+        return r;
+    }
+    const uint32_t s = a.bases[b_lo], e = a.bases[min(b_hi, nb - 1u)];
     r.lo16 = s & ~15u;
     r.n16 = ((b_hi < nb ? e : mend) + 16u - r.lo16 + 15u) >> 4;
     return r;
@@ -422,30 +429,32 @@ __device__ __forceinline__ void layout0_body(BlockArgs a, uint32_t nth, uint32_t
     const uint32_t ng = min(a.G, f.groups() - rg0);
     const uint32_t nt = ng * f.CB, tl = nt - 1u;              // look-ahead past the tile re-reads block tl
     const uint32_t B0 = rg0 * f.CB, nb = f.nb;
-    const uint32_t mend = B0 + nt == nb ? matrix_end(a, nb) : 0u;
+    const uint32_t mend = !a.stride && B0 + nt == nb ? matrix_end(a, nb) : 0u;
     // request order: region bounds and table first, then the stream copy (which needs the bounds), then the raw rows
     // and activations; loads complete in order, so each wait below covers only what it needs
     uint32_t t = hw / SP;
     const uint32_t r0 = PART ? NR * jfix : (hw % SP) * NR;    // first row of this half-wave's share of the block
-    const RowFinish fin = PART ? row_finish_load<MODE>(a, rg0 * kRows0 + r0, NR, flags)
-                               : row_finish_load<MODE>(a, rg0 * kRows0, ng * kRows0, flags);
     Coord0 c = coord0(min(t, tl), rg0, f, L);
-    Region R = region_of(a, B0, B0 + min(HB, nt), nb, mend);
+    Region R = region_of(a, B0, B0 + min(HB, nt), nb, mend, a.stride);
     if constexpr (!PIPE) {
-        // raw-plane offsets from this half-wave's first row on, computed before any vector load is requested: the
-        // compiler may use a register with a load in flight as the don't-care high half of a 64-bit multiply-add
-        // operand, and would then wait for that load.  (After the scalar loads of the region bounds: the empty asm
-        // counts as a memory write, which would turn later uniform loads into vector loads.)
+        // the block index and raw-plane offsets from this half-wave's first row on, computed before any vector load
+        // is requested: the compiler may use a register with a load in flight as the don't-care high half of a 64-bit
+        // multiply-add operand (c.b's), and would then wait for that load.  (After the scalar loads of the region
+        // bounds: the empty asm counts as a memory write, which would turn later uniform loads into vector loads.)
         c.rb += r0 * f.K16;
-        asm volatile("" : "+v"(c.rb));
+        asm volatile("" : "+v"(c.rb), "+v"(c.b));
     }
     TabStage<PEEK> Q;
     Q.issue(a, nth);
-    uint32_t n = a.hdr[(uint64_t)c.b * kHdrBytes + L], base = a.bases[c.b];
+    uint32_t n = a.hdr[(uint64_t)c.b * kHdrBytes + L], base = block_base(a, c.b);
     Bulk Bk;
     bulk_issue(Bk, a.data, R, tid, nth);
     XRegs<XBF16> x;
     if (ROWS) load_x16<XBF16>(x, a.x, c.col0, c.col_ok);
+    // the finish's scale and bias after the streams: the preloaded kernels read those pointers from their argument
+    // struct, and the wait for that read must not hold back the requests above
+    const RowFinish fin = PART ? row_finish_load<MODE>(a, rg0 * kRows0 + r0, NR, flags)
+                               : row_finish_load<MODE>(a, rg0 * kRows0, ng * kRows0, flags);
 
     if constexpr (!PIPE) {
         // everything but the raw rows is requested before the first wait; rows 0-1 once the workgroup's streams are
@@ -479,8 +488,8 @@ __device__ __forceinline__ void layout0_body(BlockArgs a, uint32_t nth, uint32_t
 #pragma unroll
         for (int r = 0; r < 4; r++) ring[r] = MODE == kRowIndex ? make_uint4(0u, 0u, 0u, 0u) : raw_row<ELEM>(a.low, f, c, r);
         Coord0 cn = coord0(min(t + H, tl), rg0, f, L);
-        uint32_t n_n = a.hdr[(uint64_t)cn.b * kHdrBytes + L], base_n = a.bases[cn.b];
-        Region Rn = region_of(a, B0 + min(H, tl), B0 + min(2u * H, nt), nb, mend);
+        uint32_t n_n = a.hdr[(uint64_t)cn.b * kHdrBytes + L], base_n = block_base(a, cn.b);
+        Region Rn = region_of(a, B0 + min(H, tl), B0 + min(2u * H, nt), nb, mend, a.stride);
         Q.commit(s, nth);
         Q.finish(s, a, nth);
         if (R.n16 * 4u <= cap) bulk_commit(Bk, cur, R, tid, nth);
@@ -490,8 +499,8 @@ __device__ __forceinline__ void layout0_body(BlockArgs a, uint32_t nth, uint32_t
         for (uint32_t k = 0;; k++) {
             // round k + 2: this half-wave's header byte and base, and the region bounds
             const Coord0 cnn = coord0(min(t + 2u * H, tl), rg0, f, L);
-            const uint32_t n_nn = a.hdr[(uint64_t)cnn.b * kHdrBytes + L], base_nn = a.bases[cnn.b];
-            const Region Rnn = region_of(a, B0 + min((k + 2u) * H, tl), B0 + min((k + 3u) * H, nt), nb, mend);
+            const uint32_t n_nn = a.hdr[(uint64_t)cnn.b * kHdrBytes + L], base_nn = block_base(a, cnn.b);
+            const Region Rnn = region_of(a, B0 + min((k + 2u) * H, tl), B0 + min((k + 3u) * H, nt), nb, mend, a.stride);
             const bool valid = t < nt;
             XRegs<XBF16> xn;
             float v;
@@ -535,19 +544,28 @@ __global__ void __launch_bounds__(1024) k_layout0(BlockArgs a) {
 
 // The single-round token kernel (BF16 x, 13-bit table) with the inputs of its first requests as leading scalar
 // arguments, which gfx950 preloads into SGPRs (the library is built with -amdgpu-kernarg-preload-count): no wave waits
-// for a kernarg read before requesting the table, header bytes, activations and region bounds (4B sweep 1685 -> 1644
-// us per token).  pk = G | H << 16 | has_scale << 30 | has_bias << 31, H = the workgroup's half-waves; everything else
-// comes from `a`, whose copies of these fields are ignored.
+// for a kernarg read before requesting the table, header bytes, activations and streams (4B sweep 1685 -> 1644 us per
+// token).  The eight arguments fill the 14 SGPRs gfx950 preloads next to the kernarg pointer; the row index, whose
+// first use comes after the streams are in LDS, is read from `a`.  With fixed slots the stream copy needs only `data`
+// and pk; otherwise it waits for the region bounds read from `bases`.
+// pk = G | H << 16 | stride / 16 << 22 | has_scale << 30 | has_bias << 31, H = the workgroup's half-waves (at most
+// 32), stride = the fixed-slot stride or 0; everything else comes from `a`, whose copies of these fields are ignored.
+__device__ __forceinline__ void take_preloaded(BlockArgs &a, const uint8_t *data, const uint32_t *bases,
+                                               const uint32_t *seq, uint32_t M, uint32_t K, uint32_t pk,
+                                               const uint8_t *hdr, const void *xp) {
+    a.data = data; a.bases = bases; a.seq = seq; a.M = M; a.K = K; a.hdr = hdr; a.x = xp;
+    a.stride = ((pk >> 22) & 0xFFu) * 16u;
+}
 template <int ELEM, int NR>
-__global__ void __launch_bounds__(1024) k_layout0p(const uint32_t *__restrict__ bases, const uint32_t *__restrict__ seq,
+__global__ void __launch_bounds__(1024) k_layout0p(const uint8_t *__restrict__ data, const uint32_t *__restrict__ bases,
+                                                   const uint32_t *__restrict__ seq, uint32_t M, uint32_t K, uint32_t pk,
                                                    const uint8_t *__restrict__ hdr, const void *__restrict__ xp,
-                                                   uint32_t M, uint32_t K, uint32_t pk, const uint16_t *__restrict__ aux,
                                                    BlockArgs a) {
     __shared__ LutT<kPeekSeq> s;
     extern __shared__ uint32_t dyn[];
-    a.bases = bases; a.seq = seq; a.hdr = hdr; a.x = xp; a.M = M; a.K = K; a.aux = aux;
+    take_preloaded(a, data, bases, seq, M, K, pk, hdr, xp);
     a.G = pk & 0xFFFFu;
-    layout0_body<ELEM, kToken, true, false, NR, kPeekSeq>(a, ((pk >> 16) & 0x3FFFu) * 32u, pk >> 30, blockIdx.x * a.G, 0u,
+    layout0_body<ELEM, kToken, true, false, NR, kPeekSeq>(a, ((pk >> 16) & 0x3Fu) * 32u, pk >> 30, blockIdx.x * a.G, 0u,
                                                           s, dyn);
 }
 
@@ -556,19 +574,20 @@ __global__ void __launch_bounds__(1024) k_layout0p(const uint32_t *__restrict__ 
 // 8 / TS each, from the row index) of the remaining row groups go one to a workgroup, so every CU decodes about the
 // same rows instead of some CUs two whole row groups (Qwen3-4B down and o_proj: 320 row groups on 256 CUs).  A part's
 // workgroup stages its row group's streams whole, so those streams are read TS times (from L2 / the MALL after the
-// first).  pk = nfull | H << 16 | has_scale << 30 | has_bias << 31 (scale and bias: token path only).
+// first).  pk = nfull | H << 16 | stride / 16 << 22 | has_scale << 30 | has_bias << 31 (scale and bias: token path
+// only; stride as for k_layout0p).
 template <int ELEM, int NRF, int TS, int MODE = kToken>
-__global__ void __launch_bounds__(1024) k_layout0t(const uint32_t *__restrict__ bases, const uint32_t *__restrict__ seq,
+__global__ void __launch_bounds__(1024) k_layout0t(const uint8_t *__restrict__ data, const uint32_t *__restrict__ bases,
+                                                   const uint32_t *__restrict__ seq, uint32_t M, uint32_t K, uint32_t pk,
                                                    const uint8_t *__restrict__ hdr, const void *__restrict__ xp,
-                                                   uint32_t M, uint32_t K, uint32_t pk, const uint16_t *__restrict__ aux,
                                                    BlockArgs a) {
     static_assert(TS == 2 || TS == 4, "halves or quarters of a row group");
     static_assert(MODE == kToken || MODE == kDequant, "token path or dequantization");
     __shared__ LutT<kPeekSeq> s;
     extern __shared__ uint32_t dyn[];
-    a.bases = bases; a.seq = seq; a.hdr = hdr; a.x = xp; a.M = M; a.K = K; a.aux = aux;
+    take_preloaded(a, data, bases, seq, M, K, pk, hdr, xp);
     a.G = 1;
-    const uint32_t nfull = pk & 0xFFFFu, nth = ((pk >> 16) & 0x3FFFu) * 32u, flags = pk >> 30;
+    const uint32_t nfull = pk & 0xFFFFu, nth = ((pk >> 16) & 0x3Fu) * 32u, flags = pk >> 30;
     if (blockIdx.x < nfull) {
         layout0_body<ELEM, MODE, true, false, NRF, kPeekSeq>(a, nth, flags, blockIdx.x, 0u, s, dyn);
     } else {
@@ -579,9 +598,10 @@ __global__ void __launch_bounds__(1024) k_layout0t(const uint32_t *__restrict__ 
 
 template <int ELEM, int NRF, int TS, int MODE>
 static void launch_layout0t(const LaunchPlan &p, const BlockArgs &a, hipStream_t st) {
-    const uint32_t pk = p.G | ((p.threads / 32u) << 16) | (a.scale ? 1u << 30 : 0u) | (a.bias ? 1u << 31 : 0u);
-    hipLaunchKernelGGL((k_layout0t<ELEM, NRF, TS, MODE>), dim3(p.grid), dim3(p.threads), p.lds, st, a.bases, a.seq,
-                       a.hdr, a.x, a.M, a.K, pk, a.aux, a);
+    const uint32_t pk = p.G | ((p.threads / 32u) << 16) | ((a.stride >> 4) << 22) | (a.scale ? 1u << 30 : 0u) |
+                        (a.bias ? 1u << 31 : 0u);
+    hipLaunchKernelGGL((k_layout0t<ELEM, NRF, TS, MODE>), dim3(p.grid), dim3(p.threads), p.lds, st, a.data, a.bases,
+                       a.seq, a.M, a.K, pk, a.hdr, a.x, a);
 }
 
 // the split-tail plan's kernel by rows per half-wave of a whole row group (8 / split) and parts per row group
@@ -602,9 +622,10 @@ static int launch_layout0_tail(const LaunchPlan &p, const BlockArgs &a, hipStrea
 
 template <int ELEM, int NR>
 static void launch_layout0p(const LaunchPlan &p, const BlockArgs &a, hipStream_t st) {
-    const uint32_t pk = p.G | ((p.threads / 32u) << 16) | (a.scale ? 1u << 30 : 0u) | (a.bias ? 1u << 31 : 0u);
-    hipLaunchKernelGGL((k_layout0p<ELEM, NR>), dim3(p.grid), dim3(p.threads), p.lds, st, a.bases, a.seq, a.hdr, a.x,
-                       a.M, a.K, pk, a.aux, a);
+    const uint32_t pk = p.G | ((p.threads / 32u) << 16) | ((a.stride >> 4) << 22) | (a.scale ? 1u << 30 : 0u) |
+                        (a.bias ? 1u << 31 : 0u);
+    hipLaunchKernelGGL((k_layout0p<ELEM, NR>), dim3(p.grid), dim3(p.threads), p.lds, st, a.data, a.bases, a.seq,
+                       a.M, a.K, pk, a.hdr, a.x, a);
 }
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -912,7 +933,7 @@ __device__ __forceinline__ void layout1s_body(BlockArgs a, uint32_t nth, uint32_
     const uint32_t nt = ng * f.CB, tl = nt - 1u;
     const uint32_t B0 = rg0 * f.CB, nb = f.nb;
     const uint32_t mend = B0 + nt == nb ? matrix_end(a, nb) : 0u;
-    Region R = region_of(a, B0, B0 + nt, nb, mend);
+    Region R = region_of(a, B0, B0 + nt, nb, mend, 0u);
     TabStage<PEEK> Q;
     Q.issue(a, nth);
     const uint32_t t = hw / SP, p = hw % SP, sc0 = p * NS;
@@ -1002,7 +1023,7 @@ __device__ __forceinline__ void layout1m_body(BlockArgs a, uint32_t nth, uint32_
     float *part = (float *)(xs + n8);
     const uint32_t B0 = rg0 * f.CB, nb = f.nb;
     const uint32_t mend = B0 + nt == nb ? matrix_end(a, nb) : 0u;
-    Region R = region_of(a, B0, B0 + nt, nb, mend);
+    Region R = region_of(a, B0, B0 + nt, nb, mend, 0u);
     TabStage<PEEK> Q;
     Q.issue(a, nth);
     const uint32_t ntot = nt * SP, itl = ntot - 1u;
@@ -1198,7 +1219,8 @@ template <int ELEM, int PEEK>
 static int launch_layout1_token(const LaunchPlan &p, const BlockArgs &a, hipStream_t st, bool full) {
     const dim3 g(p.grid), b(p.threads);
     // the preloaded kernels' packed word: tile, half-waves, scale and bias present
-    const uint32_t pk = p.G | ((p.threads / 32u) << 16) | (a.scale ? 1u << 30 : 0u) | (a.bias ? 1u << 31 : 0u);
+    const uint32_t pk = p.G | ((p.threads / 32u) << 16) | ((a.stride >> 4) << 22) | (a.scale ? 1u << 30 : 0u) |
+                        (a.bias ? 1u << 31 : 0u);
 #define NWC_L1_PRELOAD a.bases, a.seq, a.hdr, a.x, a.M, a.K, pk, a.aux, a
     if (p.multi) {
         // more than 64 KB of LDS: raise the kernel's limit (idempotent, so concurrent first calls are fine)
@@ -1376,7 +1398,7 @@ __global__ void __launch_bounds__(1024) k_layout0_batch(BlockArgs a) {
     const uint32_t ng = min(a.G, f.groups() - rg0);
     const uint32_t nt = ng * f.CB, tl = nt - 1u;
     const uint32_t B0 = rg0 * f.CB, nb = f.nb;
-    const uint32_t mend = B0 + nt == nb ? matrix_end(a, nb) : 0u;
+    const uint32_t mend = !a.stride && B0 + nt == nb ? matrix_end(a, nb) : 0u;
     const uint32_t t = hw;
     // fp8: the scale and bias of this thread's first output (row rg0 * 8 + tid / NT), requested first (as
     // row_finish_load does)
@@ -1386,10 +1408,10 @@ __global__ void __launch_bounds__(1024) k_layout0_batch(BlockArgs a) {
         if (a.bias) fin_bias = __uint_as_float((uint32_t)a.bias[rg0 * kRows0 + tid / NT] << 16);
     }
     const Coord0 c = coord0(min(t, tl), rg0, f, L);
-    const Region R = region_of(a, B0, B0 + min(H, nt), nb, mend);
+    const Region R = region_of(a, B0, B0 + min(H, nt), nb, mend, a.stride);
     TabStage<PEEK> Q;
     Q.issue(a);
-    const uint32_t n = a.hdr[(uint64_t)c.b * kHdrBytes + L], base = a.bases[c.b];
+    const uint32_t n = a.hdr[(uint64_t)c.b * kHdrBytes + L], base = block_base(a, c.b);
     Bulk Bk;
     bulk_issue(Bk, a.data, R, tid, nth);
     XRegs<true> x[NT];

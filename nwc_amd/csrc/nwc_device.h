@@ -449,7 +449,13 @@ struct BlockArgs {
     uint32_t G;             // row groups per workgroup
     uint32_t slot_words;    // LDS words per half-wave for a staged block (layouts 0/1)
     const uint32_t *seq;    // 13-bit token-path decode table (nwc_seq_table) or null
+    uint32_t stride;        // layout 0 in fixed slots: block b's streams at byte b * stride (elem_stride); 0 = bases[b]
 };
+
+// Byte offset of block b's streams: computed for fixed slots, else bases[b] (a scalar load the stream copy waits for).
+__device__ __forceinline__ uint32_t block_base(const BlockArgs &a, uint32_t b) {
+    return a.stride ? b * a.stride : a.bases[b];
+}
 
 // Prefill without a temporary BF16 matrix (k_prefill0): the matrix in `a` (a.out = y [T x M] BF16, a.aux = row index,
 // a.seq = 13-bit table, both required), activations [T x K16] BF16.

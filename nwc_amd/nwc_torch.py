@@ -38,6 +38,12 @@ LAYOUTS = (0, 1, 2)
 _default_layout = int(os.environ.get("NWC_LAYOUT", "0"))
 LAYOUT_DEFAULT = {ELEM_BF16: _default_layout, ELEM_FP8: _default_layout}
 SEQ_TABLE = os.environ.get("NWC_SEQ_TABLE", "1") != "0"   # layouts 0/1: stage the 13-bit decode table
+# layout 0 on a GPU: each block's streams in a slot of one fixed stride, so the token kernels compute a block's offset
+# instead of reading it before they can request the streams (Qwen3-4B sweep 1555-1579 -> 1529-1538 us per token)
+FIXED_SLOTS = os.environ.get("NWC_FIXED_SLOTS", "1") != "0"
+SLOT_MAX = 1728                   # the library's largest stride (nwc_format.h kSlotMax)
+SLOT_OVERHEAD = 1.06              # slots only where they hold at most 6% more bytes than the packed streams
+SLOT_TAIL = 2 * DATA_SLACK        # zero bytes after the last slot (the packed form keeps 64 + DATA_SLACK)
 ROW_INDEX = os.environ.get("NWC_ROW_INDEX", "1") != "0"   # layouts 0/1: build the row index for the token path
 # layout 0: inputs of 2..BATCH_MAX tokens go through the fused kernel (four vectors per launch) instead of a
 # temporary BF16 matrix + F.linear
@@ -189,6 +195,21 @@ def _validate_streams(bases, hdr, data_len, layout, elem):
         raise ValueError("compressed streams run past the data tensor: corrupt checkpoint")
 
 
+def _block_spans(bases, hdr):
+    """int64 byte offset and byte length of every block's lane streams (layouts 0/1: four bytes per header word)."""
+    start = bases.to(torch.int64) & 0xFFFFFFFF
+    return start, hdr.view(-1, LANES).to(torch.int64).sum(1) * 4
+
+
+def _copy_spans(src, dst, src_start, dst_start, size, chunk=2048):
+    """dst[dst_start[b] + j] = src[src_start[b] + j] for every block b and j < size[b], a chunk of blocks at a time."""
+    j = torch.arange(int(size.max()), device=src.device)
+    for b0 in range(0, size.numel(), chunk):
+        part = slice(b0, b0 + chunk)
+        keep = j[None, :] < size[part, None]
+        dst[(dst_start[part, None] + j[None, :])[keep]] = src[(src_start[part, None] + j[None, :])[keep]]
+
+
 # ---------------------------------------------------------------------------------------------------------------
 
 class NWCWeight:
@@ -231,6 +252,7 @@ class NWCWeight:
         self.n = rows * cols
         self.block = block or choose_block(self.n)
         self.elem, self.layout = kind, layout
+        self._slot, self._packed = 0, None
 
     def _place(self, stored, scale, device, geo):
         for name in ("data", "bases", "hdr", "lut", "low"):
@@ -241,6 +263,29 @@ class NWCWeight:
         self._scratch = self._row_index = self._seq_table = None
         self.bytes_bf16 = 2 * self.n
         self.bytes_native = self.n + 4 * self.out_features if self.elem == ELEM_FP8 else 2 * self.n
+        self._packed_len = self.data.numel()
+        if self.layout == 0 and FIXED_SLOTS and self.data.device.type == "cuda" and self.bases.numel():
+            self._to_slots()
+
+    def _to_slots(self):
+        """Move layout 0's block streams into slots of one stride (the largest block's bytes, rounded up to 16):
+        block b at byte b * stride, so bases[b] = b * stride, which is still a valid tensor set of the format.  Kept
+        packed when the slots would hold more than SLOT_OVERHEAD times the bytes, when the stride passes SLOT_MAX, or
+        when `data` holds non-zero bytes outside the blocks' streams (tensors() could not restore it exactly)."""
+        start, size = _block_spans(self.bases, self.hdr)
+        nb = size.numel()
+        stride = -(-int(size.max()) // 16) * 16
+        if not 0 < stride <= SLOT_MAX or nb * stride > SLOT_OVERHEAD * self._packed_len \
+                or nb * stride + SLOT_TAIL >= 1 << 32:
+            return
+        slots = torch.zeros(nb * stride + SLOT_TAIL, dtype=torch.uint8, device=self.data.device)
+        first = torch.arange(nb, device=self.data.device, dtype=torch.int64) * stride
+        _copy_spans(self.data, slots, start, first, size)
+        # the copy holds every stream byte, so equal sums mean every byte outside the streams is zero
+        if int(slots.sum(dtype=torch.int64)) != int(self.data.sum(dtype=torch.int64)):
+            return
+        self._packed = self.bases
+        self.data, self.bases, self._slot = slots, first.to(torch.int32), stride
 
     def _stored_bytes(self, stream_bytes):
         """Compressed size: streams + bases + header + table + raw plane (+ fp8 scale), the reference's `bytes`."""
@@ -272,21 +317,28 @@ class NWCWeight:
         if low.numel() == geo.raw_bytes:
             low = F.pad(low, (0, RAW_SLACK))
         self._place({"data": data, "bases": bases, "hdr": hdr, "lut": lut, "low": low}, scale, device, geo)
-        self.bytes = self._stored_bytes(self.data.numel())
+        self.bytes = self._stored_bytes(self._packed_len)
         self._derive()
         return self
 
     def tensors(self):
-        """The stored tensors (what a checkpoint keeps)."""
+        """The stored tensors (what a checkpoint keeps); streams in fixed slots are packed back to the bytes they
+        were placed from."""
         out = {name: getattr(self, name) for name in ("data", "bases", "hdr", "lut", "low")}
+        if self._slot:
+            start, size = _block_spans(self._packed, self.hdr)
+            data = torch.zeros(self._packed_len, dtype=torch.uint8, device=self.data.device)
+            _copy_spans(self.data, data, self.bases.to(torch.int64), start, size)
+            out["data"], out["bases"] = data, self._packed
         if self.scale is not None:
             out["scale"] = self.scale
         return out
 
     @property
     def code(self):
-        """The library's `elem` argument: element type in bits 0-3, layout in bits 4-7."""
-        return self.elem | (self.layout << 4)
+        """The library's `elem` argument: element type in bits 0-3, layout in bits 4-7, the fixed-slot stride / 16
+        in bits 8-15 (0: blocks at bases[])."""
+        return self.elem | (self.layout << 4) | (self._slot // 16) << 8
 
     @property
     def scratch(self):

@@ -28,10 +28,12 @@ def bits16(t):
 
 
 def oracle_encoding(c):
-    """The oracle's view of an NWCWeight's tensors (for or_decode / or_linear)."""
-    return {"data": c.data.cpu().numpy(), "bases": c.bases.cpu().numpy().view(np.uint32), "hdr": c.hdr.cpu().numpy(),
-            "lut": c.lut.cpu().numpy().view(np.uint32), "low": c.low.cpu().numpy(), "M": c.out_features,
-            "K": c.in_features, "elem": c.elem, "layout": c.layout}
+    """The oracle's view of an NWCWeight's stored tensors (for or_decode / or_linear): the checkpoint form, with
+    layout 0's streams packed back from their fixed slots."""
+    t = c.tensors()
+    return {"data": t["data"].cpu().numpy(), "bases": t["bases"].cpu().numpy().view(np.uint32),
+            "hdr": t["hdr"].cpu().numpy(), "lut": t["lut"].cpu().numpy().view(np.uint32), "low": t["low"].cpu().numpy(),
+            "M": c.out_features, "K": c.in_features, "elem": c.elem, "layout": c.layout}
 
 
 BF16_MAX = float.fromhex("0x1.fep127")

@@ -1,0 +1,87 @@
+"""Layout 0 in fixed slots against the same matrix packed, on the GPU: every layout-0 entry point (token path with BF16
+and fp32 activations, with scale and bias; dequantization with and without the 13-bit table; the batched token
+kernel; the fused prefill; both gathers; the row-index build) gives the same bits from either placement, over the
+plans the Qwen3-4B shapes take (k_layout0p with four and eight rows per half-wave, the split tail k_layout0t, one
+workgroup per CU) and the two-buffer plan of a wide matrix.  The packed twin is rebuilt from the slot weight's
+checkpoint tensors with the slots switched off, so both decode the same bytes."""
+import numpy as np
+import pytest
+import torch
+
+from tests.helpers import bf16_matrix, oracle_encoding
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = [
+    (6144, 2560, "bf16"),     # qkv: k_layout0p, four rows per half-wave
+    (2560, 4096, "bf16"),     # o: split tail, two rows per half-wave of a whole row group + quarters
+    (19456, 2560, "bf16"),    # gate_up: k_layout0p, eight rows per half-wave
+    (2560, 9728, "fp8"),      # down as fp8 (row scale): split tail, eight rows + quarters
+    (64, 20480, "bf16"),      # 40 column blocks: the two-buffer plan
+    (1000, 2560, "fp8"),
+]
+
+
+def _twins(M, K, elem, monkeypatch):
+    import nwc_amd.nwc_torch as N
+    # fp8 without the 1e30 stressors: a row holding one quantizes to zeros, and such short row groups would keep
+    # the matrix packed (the slots would hold more than 6% padding)
+    w = bf16_matrix(M, K, seed=M + K, escapes=elem != "fp8")
+    if elem == "fp8":
+        q, s = N.quantize_fp8(w.float())
+        c = N.NWCWeight(q, device="cuda:0", elem="fp8", scale=s, layout=0)
+    else:
+        c = N.NWCWeight(w, device="cuda:0", layout=0)
+    assert c._slot, "expected fixed slots for this matrix"
+    t = c.tensors()
+    with monkeypatch.context() as m:
+        m.setattr(N, "FIXED_SLOTS", False)
+        p = N.NWCWeight.from_tensors(M, K, c.block, t["data"], t["bases"], t["hdr"], t["lut"], t["low"],
+                                     device="cuda:0", elem=elem, scale=t.get("scale"), layout=0)
+    assert p._slot == 0 and p.code == c.code & 0xFF
+    return c, p
+
+
+def _same(a, b, what):
+    assert torch.equal(a.view(torch.int16) if a.dtype == torch.bfloat16 else a,
+                       b.view(torch.int16) if b.dtype == torch.bfloat16 else b), what
+
+
+@pytest.mark.parametrize("M,K,elem", SHAPES)
+def test_slots_match_packed(cuda, M, K, elem, monkeypatch):
+    print(f"slots vs packed {M}x{K} {elem}", flush=True)
+    c, p = _twins(M, K, elem, monkeypatch)
+    assert torch.equal(c.row_index(), p.row_index())
+    g = torch.Generator().manual_seed(7)
+    x = torch.randn(K, generator=g).to(torch.bfloat16).to(cuda)
+    bias = (torch.randn(M, generator=g) * 0.1).to(torch.bfloat16).to(cuda)
+    for b in (None, bias):
+        _same(c.linear_bf16(x, b), p.linear_bf16(x, b), "token path, BF16 x")
+        _same(c.linear_bf16(x.float(), b), p.linear_bf16(x.float(), b), "token path, fp32 x")
+    _same(c.matvec(x.float()), p.matvec(x.float()), "fp32 path")
+    d = c.dequant()
+    _same(d, p.dequant(), "dequantization")
+    ids = torch.randint(0, M, (9,), generator=g).to(cuda)
+    _same(c.gather(ids), p.gather(ids), "gather")
+    if K <= 16384:
+        xs = torch.randn(3, K, generator=g).to(torch.bfloat16).to(cuda)
+        _same(c.linear_batch(xs, bias), p.linear_batch(xs, bias), "batched token path")
+        xt = torch.randn(5, K, generator=g).to(torch.bfloat16).to(cuda)
+        _same(c.prefill(xt, bias), p.prefill(xt, bias), "fused prefill")
+    if M * K <= 4096 * 2560:
+        assert np.array_equal(d.cpu().view(torch.int16).numpy().view(np.uint16), O.decode(oracle_encoding(c))), \
+            "dequantization != oracle"
+
+
+def test_dequant_without_table_matches(cuda, monkeypatch):
+    """nwc_dequant (the reference's entry point: no row index, no 13-bit table) on slots and packed."""
+    import nwc_amd.nwc_torch as N
+    c, p = _twins(2560, 4096, "bf16", monkeypatch)
+    outs = []
+    for w in (c, p):
+        out = torch.empty(w.out_features, w.K16, dtype=torch.bfloat16, device=cuda)
+        N.call("nwc_dequant", N.stream(), *w._streams(), N.ptr(out), w.n, w.block, w.in_features, w.code)
+        outs.append(out)
+    _same(outs[0], outs[1], "nwc_dequant")
+    _same(outs[0], c.dequant(), "nwc_dequant against nwc_dequant_seq")
