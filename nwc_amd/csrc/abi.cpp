@@ -37,17 +37,16 @@ int current_cus() {
 // This build also addresses the raw planes with 32-bit offsets: layout 0 counts weights of the padded matrix
 // (Mp * K16, rows past M included), layouts 1/2 count bytes of the plane padded to 16 rows and 32 columns plus its
 // 512 slack bytes; both must stay below 2^32.
-// Bits 8-15 of elem (a fixed-slot stride, layout 0 only) are this build's; the reference's callers leave them zero.
+// Bits 8-15 of elem (a fixed-slot stride, layouts 0/1) are this build's; the reference's callers leave them zero.
 bool shape_ok(uint64_t n, uint32_t block, uint32_t K, int elem) {
     if (!(block == kBlock && K != 0 && n % K == 0 && n / K >= 1 && n / K <= 0xFFFFFFFFull && elem_type(elem) <= 1 &&
-          elem_layout(elem) <= 2 && (elem & ~0xFFFF) == 0 && (elem_layout(elem) == 0 || elem_stride(elem) == 0) &&
-          elem_stride(elem) <= kSlotMax))
+          elem_layout(elem) <= 2 && (elem & ~0xFFFF) == 0 && elem_stride(elem) <= slot_max(elem_layout(elem))))
         return false;
     const uint64_t M = n / K, K16 = (K + 15u) & ~15u;
     if (M * K16 >= (1ull << 32)) return false;          // also keeps Shape's 32-bit fields (M < 2^28) from wrapping
     const Shape f((uint32_t)M, K, elem_layout(elem));
-    if (elem_layout(elem) == 0)
-        return (uint64_t)f.Mp * f.K16 < (1ull << 32) && (uint64_t)f.nb * elem_stride(elem) + 128u < (1ull << 32);
+    if ((uint64_t)f.nb * elem_stride(elem) + 128u >= (1ull << 32)) return false;
+    if (elem_layout(elem) == 0) return (uint64_t)f.Mp * f.K16 < (1ull << 32);
     return f.low_bytes(elem) + kRawSlack < (1ull << 32);
 }
 

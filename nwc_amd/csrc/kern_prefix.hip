@@ -929,20 +929,22 @@ __device__ __forceinline__ void layout1s_body(BlockArgs a, uint32_t nth, uint32_
     float *part = (float *)(xs + (ROWS ? n8 : 0u));
     const uint32_t rg0 = blockIdx.x * a.G;
     const uint32_t ng = min(a.G, f.groups() - rg0);
-    const RowFinish fin = row_finish_load<MODE, ELEM == kElemFp8>(a, rg0 * kRows12, ng * kRows12, flags);
     const uint32_t nt = ng * f.CB, tl = nt - 1u;
     const uint32_t B0 = rg0 * f.CB, nb = f.nb;
-    const uint32_t mend = B0 + nt == nb ? matrix_end(a, nb) : 0u;
-    Region R = region_of(a, B0, B0 + nt, nb, mend, 0u);
+    const uint32_t mend = !a.stride && B0 + nt == nb ? matrix_end(a, nb) : 0u;
+    Region R = region_of(a, B0, B0 + nt, nb, mend, a.stride);
     TabStage<PEEK> Q;
     Q.issue(a, nth);
     const uint32_t t = hw / SP, p = hw % SP, sc0 = p * NS;
     const Coord1 c = coord1<ELEM>(min(t, tl), rg0, f, L);
-    const uint32_t n = a.hdr[(uint64_t)c.b * kHdrBytes + L], base = a.bases[c.b];
+    const uint32_t n = a.hdr[(uint64_t)c.b * kHdrBytes + L], base = block_base(a, c.b);
     Bulk Bk;
     bulk_issue(Bk, a.data, R, tid, nth);
     XStage<XBF16> X;
     if (ROWS) x_issue<XBF16>(X, a.x, n8, tid, nth);
+    // fp8: the finish's row scale after the streams (the preloaded kernel reads its pointer from the argument struct,
+    // and the wait for that read must not hold back the requests above)
+    const RowFinish fin = row_finish_load<MODE, ELEM == kElemFp8>(a, rg0 * kRows12, ng * kRows12, flags);
     // the raw chunks are requested once this wave's stream chunks are in, before the barrier (the first one is used
     // by the first decode step)
     const uint32_t P0 = SP == 1 ? 0u : part_start(a, c.b, sc0 / 4u, L);
@@ -987,15 +989,17 @@ __global__ void __launch_bounds__(1024) k_layout1s(BlockArgs a) {
     layout1s_body<ELEM, MODE, XBF16, NS, FULL, PEEK>(a, blockDim.x, kFinishAll);
 }
 
-// k_layout1s's token path with the inputs of its first requests preloaded into SGPRs (as k_layout0p).
+// k_layout1s's token path with the inputs of its first requests preloaded into SGPRs (as k_layout0p; the table
+// argument is the stored LUT for PEEK = 12).
 template <int ELEM, int NS, bool FULL, int PEEK>
-__global__ void __launch_bounds__(1024) k_layout1sp(const uint32_t *__restrict__ bases, const uint32_t *__restrict__ seq,
+__global__ void __launch_bounds__(1024) k_layout1sp(const uint8_t *__restrict__ data, const uint32_t *__restrict__ bases,
+                                                    const uint32_t *__restrict__ seq, uint32_t M, uint32_t K, uint32_t pk,
                                                     const uint8_t *__restrict__ hdr, const void *__restrict__ xp,
-                                                    uint32_t M, uint32_t K, uint32_t pk, const uint16_t *__restrict__ aux,
                                                     BlockArgs a) {
-    a.bases = bases; a.seq = seq; a.hdr = hdr; a.x = xp; a.M = M; a.K = K; a.aux = aux;
+    take_preloaded(a, data, bases, seq, M, K, pk, hdr, xp);
+    if (PEEK != kPeekSeq) a.lut = seq;                         // the table this kernel stages
     a.G = pk & 0xFFFFu;
-    layout1s_body<ELEM, kToken, true, NS, FULL, PEEK>(a, ((pk >> 16) & 0x3FFFu) * 32u, pk >> 30);
+    layout1s_body<ELEM, kToken, true, NS, FULL, PEEK>(a, ((pk >> 16) & 0x3Fu) * 32u, pk >> 30);
 }
 
 // Layout 1, several items per half-wave: for matrices whose row groups hold more blocks than a workgroup has
@@ -1014,7 +1018,6 @@ __device__ __forceinline__ void layout1m_body(BlockArgs a, uint32_t nth, uint32_
     const Shape f(a.M, a.K, 1);
     const uint32_t rg0 = blockIdx.x * a.G;
     const uint32_t ng = min(a.G, f.groups() - rg0);
-    const RowFinish fin = row_finish_load<MODE, ELEM == kElemFp8>(a, rg0 * kRows12, ng * kRows12, flags);
     const uint32_t nt = ng * f.CB;
     const uint32_t cap = a.slot_words * a.G * f.CB;
     const uint32_t n8 = (f.K16 + 31u) / 32u * 4u;
@@ -1022,8 +1025,8 @@ __device__ __forceinline__ void layout1m_body(BlockArgs a, uint32_t nth, uint32_
     uint4 *xs = (uint4 *)(dyn + cap);
     float *part = (float *)(xs + n8);
     const uint32_t B0 = rg0 * f.CB, nb = f.nb;
-    const uint32_t mend = B0 + nt == nb ? matrix_end(a, nb) : 0u;
-    Region R = region_of(a, B0, B0 + nt, nb, mend, 0u);
+    const uint32_t mend = !a.stride && B0 + nt == nb ? matrix_end(a, nb) : 0u;
+    Region R = region_of(a, B0, B0 + nt, nb, mend, a.stride);
     TabStage<PEEK> Q;
     Q.issue(a, nth);
     const uint32_t ntot = nt * SP, itl = ntot - 1u;
@@ -1035,10 +1038,13 @@ __device__ __forceinline__ void layout1m_body(BlockArgs a, uint32_t nth, uint32_
     Coord1 c;
     uint32_t p;
     item(hw, c, p);
-    uint32_t n = a.hdr[c.b * kHdrBytes + L], base = a.bases[c.b];
-    uint32_t P0 = p ? a.aux[(c.b * kRowIndexSplits + p - 1u) * kLanes + L] : 0u;
+    uint32_t n = a.hdr[c.b * kHdrBytes + L], base = block_base(a, c.b);
     Bulk Bk;
     bulk_issue(Bk, a.data, R, tid, nth);
+    // the row-index entry and (fp8) the finish's row scale after the streams: the preloaded kernel reads both
+    // pointers from its argument struct, and the wait for that read must not hold back the stream copy
+    uint32_t P0 = p ? a.aux[(c.b * kRowIndexSplits + p - 1u) * kLanes + L] : 0u;
+    const RowFinish fin = row_finish_load<MODE, ELEM == kElemFp8>(a, rg0 * kRows12, ng * kRows12, flags);
     // the activations are stored first, which waits for the streams; then the table and the raw chunks (an order
     // measured faster here than k_layout1s's: 2560x9728 15.8 us against 16.6-17.0, the later ones leaving the
     // compiler a register choice that waits inside the item loop)
@@ -1062,7 +1068,7 @@ __device__ __forceinline__ void layout1m_body(BlockArgs a, uint32_t nth, uint32_
         Coord1 cn;
         uint32_t pn;
         item(it + H, cn, pn);
-        const uint32_t nn = a.hdr[cn.b * kHdrBytes + L], basen = a.bases[cn.b];
+        const uint32_t nn = a.hdr[cn.b * kHdrBytes + L], basen = block_base(a, cn.b);
         const uint32_t P0n = pn ? a.aux[(cn.b * kRowIndexSplits + pn - 1u) * kLanes + L] : 0u;
         const uint32_t start = half_scan_incl(n, L) - n, sc0 = p * NS;
         float2 v = make_float2(0.f, 0.f);
@@ -1094,13 +1100,14 @@ __device__ __forceinline__ void layout1m_body(BlockArgs a, uint32_t nth, uint32_
 
 // The kernel, with the inputs of its first requests preloaded into SGPRs (as k_layout0p).
 template <int ELEM, bool FULL, int PEEK>
-__global__ void __launch_bounds__(1024) k_layout1mp(const uint32_t *__restrict__ bases, const uint32_t *__restrict__ seq,
+__global__ void __launch_bounds__(1024) k_layout1mp(const uint8_t *__restrict__ data, const uint32_t *__restrict__ bases,
+                                                    const uint32_t *__restrict__ seq, uint32_t M, uint32_t K, uint32_t pk,
                                                     const uint8_t *__restrict__ hdr, const void *__restrict__ xp,
-                                                    uint32_t M, uint32_t K, uint32_t pk, const uint16_t *__restrict__ aux,
                                                     BlockArgs a) {
-    a.bases = bases; a.seq = seq; a.hdr = hdr; a.x = xp; a.M = M; a.K = K; a.aux = aux;
+    take_preloaded(a, data, bases, seq, M, K, pk, hdr, xp);
+    if (PEEK != kPeekSeq) a.lut = seq;                         // the table this kernel stages
     a.G = pk & 0xFFFFu;
-    layout1m_body<ELEM, FULL, PEEK>(a, ((pk >> 16) & 0x3FFFu) * 32u, pk >> 30);
+    layout1m_body<ELEM, FULL, PEEK>(a, ((pk >> 16) & 0x3Fu) * 32u, pk >> 30);
 }
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -1218,10 +1225,11 @@ __global__ void __launch_bounds__(256) k_gather1(GatherArgs a) {
 template <int ELEM, int PEEK>
 static int launch_layout1_token(const LaunchPlan &p, const BlockArgs &a, hipStream_t st, bool full) {
     const dim3 g(p.grid), b(p.threads);
-    // the preloaded kernels' packed word: tile, half-waves, scale and bias present
+    // the preloaded kernels' packed word: tile, half-waves, slot stride, scale and bias present
     const uint32_t pk = p.G | ((p.threads / 32u) << 16) | ((a.stride >> 4) << 22) | (a.scale ? 1u << 30 : 0u) |
                         (a.bias ? 1u << 31 : 0u);
-#define NWC_L1_PRELOAD a.bases, a.seq, a.hdr, a.x, a.M, a.K, pk, a.aux, a
+    // the table argument: the 13-bit table or the stored LUT, whichever the kernel stages
+#define NWC_L1_PRELOAD a.data, a.bases, PEEK == kPeekSeq ? a.seq : a.lut, a.M, a.K, pk, a.hdr, a.x, a
     if (p.multi) {
         // more than 64 KB of LDS: raise the kernel's limit (idempotent, so concurrent first calls are fine)
         auto kf = full ? (const void *)k_layout1mp<ELEM, true, PEEK> : (const void *)k_layout1mp<ELEM, false, PEEK>;

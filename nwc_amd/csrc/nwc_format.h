@@ -30,13 +30,16 @@ constexpr int kElemFp8 = 1;
 
 __host__ __device__ constexpr int elem_type(int e) { return e & 15; }
 __host__ __device__ constexpr int elem_layout(int e) { return (e >> 4) & 15; }
-// Layout 0 placed in fixed slots (not a format property; the reference's callers leave bits 8-15 zero): the streams of
-// block b start at byte b * stride, so bases[b] = b * stride and `data` holds nb * stride + 128 bytes.  The token
+// Layouts 0/1 placed in fixed slots (not a format property; the reference's callers leave bits 8-15 zero): the streams
+// of block b start at byte b * stride, so bases[b] = b * stride and `data` holds nb * stride + 128 bytes.  The token
 // kernels then compute a block's offset instead of reading it.  Bits 8-15 hold stride / 16; 0 = bases[] only.
 __host__ __device__ constexpr uint32_t elem_stride(int e) { return (uint32_t)((e >> 8) & 0xFF) * 16u; }
-// Largest stride: a round of H slots plus the 16 bytes read past its end must fit the smallest region buffer the
-// layout-0 plans give a block (440 words).
-constexpr uint32_t kSlotMax = 1728;
+// Largest stride: a tile's slots plus the 16 bytes read past the last one must fit the smallest region buffer the
+// plans give a block (layout 0: 440 words; layout 1: 768 words).
+constexpr uint32_t kSlotMax0 = 1728, kSlotMax1 = 3040;
+__host__ __device__ constexpr uint32_t slot_max(int layout) {
+    return layout == 0 ? kSlotMax0 : layout == 1 ? kSlotMax1 : 0u;
+}
 
 // Rounded-up dimensions of an M x K matrix for a layout (nwc_ops.cu:87-98).
 struct Shape {

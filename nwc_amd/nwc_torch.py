@@ -38,10 +38,10 @@ LAYOUTS = (0, 1, 2)
 _default_layout = int(os.environ.get("NWC_LAYOUT", "0"))
 LAYOUT_DEFAULT = {ELEM_BF16: _default_layout, ELEM_FP8: _default_layout}
 SEQ_TABLE = os.environ.get("NWC_SEQ_TABLE", "1") != "0"   # layouts 0/1: stage the 13-bit decode table
-# layout 0 on a GPU: each block's streams in a slot of one fixed stride, so the token kernels compute a block's offset
-# instead of reading it before they can request the streams (Qwen3-4B sweep 1555-1579 -> 1529-1538 us per token)
+# layouts 0/1 on a GPU: each block's streams in a slot of one fixed stride, so the token kernels compute a block's
+# offset instead of reading it before they can request the streams (Qwen3-4B layout-0 sweep 1577 -> 1523 us per token)
 FIXED_SLOTS = os.environ.get("NWC_FIXED_SLOTS", "1") != "0"
-SLOT_MAX = 1728                   # the library's largest stride (nwc_format.h kSlotMax)
+SLOT_MAX = {0: 1728, 1: 3040}     # the library's largest stride per layout (nwc_format.h kSlotMax0 / kSlotMax1)
 SLOT_OVERHEAD = 1.06              # slots only where they hold at most 6% more bytes than the packed streams
 SLOT_TAIL = 2 * DATA_SLACK        # zero bytes after the last slot (the packed form keeps 64 + DATA_SLACK)
 ROW_INDEX = os.environ.get("NWC_ROW_INDEX", "1") != "0"   # layouts 0/1: build the row index for the token path
@@ -264,19 +264,20 @@ class NWCWeight:
         self.bytes_bf16 = 2 * self.n
         self.bytes_native = self.n + 4 * self.out_features if self.elem == ELEM_FP8 else 2 * self.n
         self._packed_len = self.data.numel()
-        if self.layout == 0 and FIXED_SLOTS and self.data.device.type == "cuda" and self.bases.numel():
+        if self.layout <= 1 and FIXED_SLOTS and self.data.device.type == "cuda" and self.bases.numel():
             self._to_slots()
 
     def _to_slots(self):
-        """Move layout 0's block streams into slots of one stride (the largest block's bytes, rounded up to 16):
-        block b at byte b * stride, so bases[b] = b * stride, which is still a valid tensor set of the format.  Kept
-        packed when the slots would hold more than SLOT_OVERHEAD times the bytes, when the stride passes SLOT_MAX, or
-        when `data` holds non-zero bytes outside the blocks' streams (tensors() could not restore it exactly)."""
+        """Move the block streams of layouts 0/1 into slots of one stride (the largest block's bytes, rounded up to
+        16): block b at byte b * stride, so bases[b] = b * stride, which is still a valid tensor set of the format.
+        Kept packed when the slots would hold more than SLOT_OVERHEAD times the bytes, when the stride passes the
+        layout's SLOT_MAX, or when `data` holds non-zero bytes outside the blocks' streams (tensors() could not restore
+        it exactly)."""
         start, size = _block_spans(self.bases, self.hdr)
         nb = size.numel()
         stride = -(-int(size.max()) // 16) * 16
-        if not 0 < stride <= SLOT_MAX or nb * stride > SLOT_OVERHEAD * self._packed_len \
-                or nb * stride + SLOT_TAIL >= 1 << 32:
+        if not 0 < stride <= SLOT_MAX[self.layout] or nb * stride > SLOT_OVERHEAD * self._packed_len \
+                or nb * stride + SLOT_TAIL >= 1 << 31:
             return
         slots = torch.zeros(nb * stride + SLOT_TAIL, dtype=torch.uint8, device=self.data.device)
         first = torch.arange(nb, device=self.data.device, dtype=torch.int64) * stride

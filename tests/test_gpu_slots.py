@@ -1,9 +1,10 @@
-"""Layout 0 in fixed slots against the same matrix packed, on the GPU: every layout-0 entry point (token path with BF16
+"""Layouts 0/1 in fixed slots against the same matrix packed, on the GPU: every entry point (token path with BF16
 and fp32 activations, with scale and bias; dequantization with and without the 13-bit table; the batched token
-kernel; the fused prefill; both gathers; the row-index build) gives the same bits from either placement, over the
-plans the Qwen3-4B shapes take (k_layout0p with four and eight rows per half-wave, the split tail k_layout0t, one
-workgroup per CU) and the two-buffer plan of a wide matrix.  The packed twin is rebuilt from the slot weight's
-checkpoint tensors with the slots switched off, so both decode the same bytes."""
+kernel and the fused prefill of layout 0; both gathers; the row-index build) gives the same bits from either
+placement, over the plans the Qwen3-4B shapes take (layout 0: k_layout0p with four and eight rows per half-wave, the
+split tail k_layout0t, one workgroup per CU, and the two-buffer plan of a wide matrix; layout 1: k_layout1sp with
+the 12-bit LUT and the 13-bit table, and the multi-item k_layout1mp).  The packed twin is rebuilt from the slot
+weight's checkpoint tensors with the slots switched off, so both decode the same bytes."""
 import numpy as np
 import pytest
 import torch
@@ -14,31 +15,35 @@ from oracle import oracle as O
 pytestmark = pytest.mark.gpu
 
 SHAPES = [
-    (6144, 2560, "bf16"),     # qkv: k_layout0p, four rows per half-wave
-    (2560, 4096, "bf16"),     # o: split tail, two rows per half-wave of a whole row group + quarters
-    (19456, 2560, "bf16"),    # gate_up: k_layout0p, eight rows per half-wave
-    (2560, 9728, "fp8"),      # down as fp8 (row scale): split tail, eight rows + quarters
-    (64, 20480, "bf16"),      # 40 column blocks: the two-buffer plan
-    (1000, 2560, "fp8"),
+    (6144, 2560, "bf16", 0),     # qkv: k_layout0p, four rows per half-wave
+    (2560, 4096, "bf16", 0),     # o: split tail, two rows per half-wave of a whole row group + quarters
+    (19456, 2560, "bf16", 0),    # gate_up: k_layout0p, eight rows per half-wave
+    (2560, 9728, "fp8", 0),      # down as fp8 (row scale): split tail, eight rows + quarters
+    (64, 20480, "bf16", 0),      # 40 column blocks: the two-buffer plan
+    (1000, 2560, "fp8", 0),
+    (6144, 2560, "bf16", 1),     # layout 1 qkv
+    (19456, 2560, "bf16", 1),    # layout 1 gate_up (12-bit LUT)
+    (2560, 9728, "bf16", 1),     # layout 1 down: the multi-item kernel
+    (2560, 4096, "fp8", 1),
 ]
 
 
-def _twins(M, K, elem, monkeypatch):
+def _twins(M, K, elem, monkeypatch, layout=0):
     import nwc_amd.nwc_torch as N
     # fp8 without the 1e30 stressors: a row holding one quantizes to zeros, and such short row groups would keep
     # the matrix packed (the slots would hold more than 6% padding)
     w = bf16_matrix(M, K, seed=M + K, escapes=elem != "fp8")
     if elem == "fp8":
         q, s = N.quantize_fp8(w.float())
-        c = N.NWCWeight(q, device="cuda:0", elem="fp8", scale=s, layout=0)
+        c = N.NWCWeight(q, device="cuda:0", elem="fp8", scale=s, layout=layout)
     else:
-        c = N.NWCWeight(w, device="cuda:0", layout=0)
+        c = N.NWCWeight(w, device="cuda:0", layout=layout)
     assert c._slot, "expected fixed slots for this matrix"
     t = c.tensors()
     with monkeypatch.context() as m:
         m.setattr(N, "FIXED_SLOTS", False)
         p = N.NWCWeight.from_tensors(M, K, c.block, t["data"], t["bases"], t["hdr"], t["lut"], t["low"],
-                                     device="cuda:0", elem=elem, scale=t.get("scale"), layout=0)
+                                     device="cuda:0", elem=elem, scale=t.get("scale"), layout=layout)
     assert p._slot == 0 and p.code == c.code & 0xFF
     return c, p
 
@@ -48,10 +53,10 @@ def _same(a, b, what):
                        b.view(torch.int16) if b.dtype == torch.bfloat16 else b), what
 
 
-@pytest.mark.parametrize("M,K,elem", SHAPES)
-def test_slots_match_packed(cuda, M, K, elem, monkeypatch):
-    print(f"slots vs packed {M}x{K} {elem}", flush=True)
-    c, p = _twins(M, K, elem, monkeypatch)
+@pytest.mark.parametrize("M,K,elem,layout", SHAPES)
+def test_slots_match_packed(cuda, M, K, elem, layout, monkeypatch):
+    print(f"slots vs packed {M}x{K} {elem} layout {layout}", flush=True)
+    c, p = _twins(M, K, elem, monkeypatch, layout)
     assert torch.equal(c.row_index(), p.row_index())
     g = torch.Generator().manual_seed(7)
     x = torch.randn(K, generator=g).to(torch.bfloat16).to(cuda)
@@ -64,7 +69,7 @@ def test_slots_match_packed(cuda, M, K, elem, monkeypatch):
     _same(d, p.dequant(), "dequantization")
     ids = torch.randint(0, M, (9,), generator=g).to(cuda)
     _same(c.gather(ids), p.gather(ids), "gather")
-    if K <= 16384:
+    if K <= 16384 and layout == 0:
         xs = torch.randn(3, K, generator=g).to(torch.bfloat16).to(cuda)
         _same(c.linear_batch(xs, bias), p.linear_batch(xs, bias), "batched token path")
         xt = torch.randn(5, K, generator=g).to(torch.bfloat16).to(cuda)

@@ -1,4 +1,4 @@
-"""Layout 0 in fixed slots (NWCWeight._to_slots, done when a matrix is placed on a GPU): every block's lane streams
+"""Layouts 0/1 in fixed slots (NWCWeight._to_slots, done when a matrix is placed on a GPU): every block's lane streams
 start at byte b * stride, so the token kernels compute a block's offset instead of reading bases[b] before they can
 request the streams.  The slot tensors must remain a valid tensor set of the format (the oracle's restatement of the
 reference decoder reads them as it reads the packed ones), tensors() must give back the packed bytes exactly, and
@@ -13,28 +13,30 @@ import torch
 from tests.helpers import bf16_matrix
 
 
-def _weight(M, K, elem="bf16", seed=5, w=None):
+def _weight(M, K, elem="bf16", seed=5, w=None, layout=0):
     pytest.importorskip("nwc_amd.nwc_torch", reason="the HIP library is not built")
     from nwc_amd.nwc_torch import NWCWeight, quantize_fp8
     w = bf16_matrix(M, K, seed=seed) if w is None else w
     if elem == "fp8":
         q, s = quantize_fp8(w.float())
-        return NWCWeight(q, device="cpu", elem="fp8", scale=s, layout=0)
-    return NWCWeight(w, device="cpu", layout=0)
+        return NWCWeight(q, device="cpu", elem="fp8", scale=s, layout=layout)
+    return NWCWeight(w, device="cpu", layout=layout)
 
 
 def _oracle_decode(c, data, bases):
     from oracle import oracle as O
     enc = {"data": data.numpy(), "bases": bases.numpy().view(np.uint32), "hdr": c.hdr.numpy(),
            "lut": c.lut.numpy().view(np.uint32), "low": c.low.numpy(), "M": c.out_features, "K": c.in_features,
-           "elem": c.elem, "layout": 0}
+           "elem": c.elem, "layout": c.layout}
     return O.decode(enc)
 
 
-@pytest.mark.parametrize("M,K,elem", [(64, 512, "bf16"), (48, 2560, "bf16"), (24, 2560, "fp8"), (16, 33, "bf16")])
-def test_slots_round_trip(M, K, elem):
+@pytest.mark.parametrize("M,K,elem,layout", [(64, 512, "bf16", 0), (48, 2560, "bf16", 0), (24, 2560, "fp8", 0),
+                                             (16, 33, "bf16", 0), (64, 2560, "bf16", 1), (32, 4096, "fp8", 1),
+                                             (32, 33, "bf16", 1)])
+def test_slots_round_trip(M, K, elem, layout):
     from nwc_amd.nwc_torch import LANES, SLOT_TAIL
-    c = _weight(M, K, elem)
+    c = _weight(M, K, elem, layout=layout)
     packed = {k: v.clone() for k, v in c.tensors().items()}
     code, size_bytes = c.code, c.bytes
     c._to_slots()
@@ -93,7 +95,7 @@ def test_wide_blocks_keep_packed():
     bits = torch.randint(-32768, 32767, (16, 1024), generator=g, dtype=torch.int32).to(torch.int16)
     bits[(bits & 0x7F80) == 0x7F80] = 0                             # no inf / NaN
     c = _weight(16, 1024, w=bits.view(torch.bfloat16))
-    assert int(c.hdr.view(-1, LANES).to(torch.int64).sum(1).max()) * 4 > SLOT_MAX
+    assert int(c.hdr.view(-1, LANES).to(torch.int64).sum(1).max()) * 4 > SLOT_MAX[0]
     before = c.data.clone()
     c._to_slots()
     assert c._slot == 0 and torch.equal(c.data, before)
@@ -113,8 +115,10 @@ def _lib():
 @pytest.mark.parametrize("M,K,elem,ok", [
     (2560, 4096, 0x00 | 94 << 8, True),          # layout 0, stride 1504
     (2560, 4096, 0x01 | 108 << 8, True),         # fp8, stride 1728 (the largest)
-    (2560, 4096, 0x00 | 109 << 8, False),        # stride 1744: past the largest
-    (2560, 4096, 0x10 | 94 << 8, False),         # layout 1 has no slots
+    (2560, 4096, 0x00 | 109 << 8, False),        # stride 1744: past layout 0's largest
+    (2560, 4096, 0x10 | 186 << 8, True),         # layout 1, stride 2976
+    (2560, 4096, 0x11 | 190 << 8, True),         # layout 1 fp8, stride 3040 (the largest)
+    (2560, 4096, 0x10 | 191 << 8, False),        # stride 3056: past layout 1's largest
     (2560, 4096, 0x20 | 94 << 8, False),         # layout 2 has no slots
     (2560, 4096, 0x00 | 1 << 16, False),         # unknown bits
     ((1 << 27) - 8, 16, 0x00 | 17 << 8, False),  # 2^24 - 1 blocks of 272-byte slots pass 2^32 bytes
