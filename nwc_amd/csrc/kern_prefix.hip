@@ -1393,11 +1393,20 @@ __device__ __forceinline__ void rows_batch(const Tab &s, const uint32_t *lane, c
     for (int t = 0; t < NT; t++) out[t] = reduce8_transposed(acc[t], L);
 }
 
+// The first inputs come as the eight preloaded scalar arguments of k_layout0p (the table argument: the table this
+// kernel stages); pk = G | H << 16 | stride / 16 << 22.
 template <int ELEM, int NT, int PEEK = kPeek>
-__global__ void __launch_bounds__(1024) k_layout0_batch(BlockArgs a) {
+__global__ void __launch_bounds__(1024) k_layout0_batch(const uint8_t *__restrict__ data,
+                                                        const uint32_t *__restrict__ bases,
+                                                        const uint32_t *__restrict__ tab, uint32_t M, uint32_t K,
+                                                        uint32_t pk, const uint8_t *__restrict__ hdr,
+                                                        const void *__restrict__ xp, BlockArgs a) {
     __shared__ LutT<PEEK> s;
     extern __shared__ uint32_t dyn[];
-    const uint32_t tid = threadIdx.x, nth = blockDim.x, L = tid & 31, hw = tid >> 5, H = nth >> 5;
+    take_preloaded(a, data, bases, tab, M, K, pk, hdr, xp);
+    if (PEEK != kPeekSeq) a.lut = tab;
+    a.G = pk & 0xFFFFu;
+    const uint32_t tid = threadIdx.x, nth = ((pk >> 16) & 0x3Fu) * 32u, L = tid & 31, hw = tid >> 5, H = nth >> 5;
     const uint32_t cap = a.slot_words * H;                    // one region slot per half-wave (one block each)
     uint32_t *cur = dyn;
     float *part = (float *)(dyn + cap);                       // [G * 8 rows][CB][NT]
@@ -1408,25 +1417,25 @@ __global__ void __launch_bounds__(1024) k_layout0_batch(BlockArgs a) {
     const uint32_t B0 = rg0 * f.CB, nb = f.nb;
     const uint32_t mend = !a.stride && B0 + nt == nb ? matrix_end(a, nb) : 0u;
     const uint32_t t = hw;
-    // fp8: the scale and bias of this thread's first output (row rg0 * 8 + tid / NT), requested first (as
-    // row_finish_load does)
-    float fin_scale = 1.f, fin_bias = 0.f;
-    if (ELEM == kElemFp8 && tid < ng * kRows0 * NT && rg0 * kRows0 + tid / NT < a.M) {
-        if (a.scale) fin_scale = a.scale[rg0 * kRows0 + tid / NT];
-        if (a.bias) fin_bias = __uint_as_float((uint32_t)a.bias[rg0 * kRows0 + tid / NT] << 16);
-    }
     const Coord0 c = coord0(min(t, tl), rg0, f, L);
     const Region R = region_of(a, B0, B0 + min(H, nt), nb, mend, a.stride);
     TabStage<PEEK> Q;
-    Q.issue(a);
+    Q.issue(a, nth);
     const uint32_t n = a.hdr[(uint64_t)c.b * kHdrBytes + L], base = block_base(a, c.b);
     Bulk Bk;
     bulk_issue(Bk, a.data, R, tid, nth);
     XRegs<true> x[NT];
 #pragma unroll
     for (int v = 0; v < NT; v++) load_x16<true>(x[v], (const uint16_t *)a.x + (uint64_t)v * f.K16, c.col0, c.col_ok);
-    Q.commit(s);
-    Q.finish(s, a);
+    // fp8: the scale and bias of this thread's first output (row rg0 * 8 + tid / NT), requested after the streams
+    // (their pointers are read from the argument struct, and the wait for that read must not hold back the copy)
+    float fin_scale = 1.f, fin_bias = 0.f;
+    if (ELEM == kElemFp8 && tid < ng * kRows0 * NT && rg0 * kRows0 + tid / NT < a.M) {
+        if (a.scale) fin_scale = a.scale[rg0 * kRows0 + tid / NT];
+        if (a.bias) fin_bias = __uint_as_float((uint32_t)a.bias[rg0 * kRows0 + tid / NT] << 16);
+    }
+    Q.commit(s, nth);
+    Q.finish(s, a, nth);
     const bool fits = R.n16 * 4u <= cap;
     if (fits) bulk_commit(Bk, cur, R, tid, nth);
     uint4 ring[kRing0];                                         // once this wave's stream chunks are in
@@ -1444,7 +1453,7 @@ __global__ void __launch_bounds__(1024) k_layout0_batch(BlockArgs a) {
         }
     }
     __syncthreads();
-    for (uint32_t i = threadIdx.x; i < ng * kRows0 * NT; i += blockDim.x) {
+    for (uint32_t i = threadIdx.x; i < ng * kRows0 * NT; i += nth) {
         const uint32_t u = i % NT, rr = i / NT, row = rg0 * kRows0 + rr;
         if (row >= a.M) continue;
         float acc = 0.f;
@@ -1459,12 +1468,16 @@ __global__ void __launch_bounds__(1024) k_layout0_batch(BlockArgs a) {
 template <int ELEM, int PEEK>
 static int launch_batch_t(const LaunchPlan &p, const BlockArgs &a, uint32_t ntok, hipStream_t st) {
     const dim3 g(p.grid), b(p.threads);
+    const uint32_t pk = p.G | ((p.threads / 32u) << 16) | ((a.stride >> 4) << 22);
+    const uint32_t *tab = PEEK == kPeekSeq ? a.seq : a.lut;
+#define NWC_B_PRELOAD a.data, a.bases, tab, a.M, a.K, pk, a.hdr, a.x, a
     switch (ntok) {
-    case 2: hipLaunchKernelGGL((k_layout0_batch<ELEM, 2, PEEK>), g, b, p.lds, st, a); break;
-    case 3: hipLaunchKernelGGL((k_layout0_batch<ELEM, 3, PEEK>), g, b, p.lds, st, a); break;
-    case 4: hipLaunchKernelGGL((k_layout0_batch<ELEM, 4, PEEK>), g, b, p.lds, st, a); break;
+    case 2: hipLaunchKernelGGL((k_layout0_batch<ELEM, 2, PEEK>), g, b, p.lds, st, NWC_B_PRELOAD); break;
+    case 3: hipLaunchKernelGGL((k_layout0_batch<ELEM, 3, PEEK>), g, b, p.lds, st, NWC_B_PRELOAD); break;
+    case 4: hipLaunchKernelGGL((k_layout0_batch<ELEM, 4, PEEK>), g, b, p.lds, st, NWC_B_PRELOAD); break;
     default: return -1;
     }
+#undef NWC_B_PRELOAD
     return (int)hipGetLastError();
 }
 
