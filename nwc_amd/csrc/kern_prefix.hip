@@ -542,8 +542,9 @@ __global__ void __launch_bounds__(1024) k_layout0(BlockArgs a) {
     layout0_body<ELEM, MODE, XBF16, PIPE, NR, PEEK>(a, blockDim.x, kFinishAll, blockIdx.x * a.G, 0u, s, dyn);
 }
 
-// The single-round token kernel (BF16 x, 13-bit table) with the inputs of its first requests as leading scalar
-// arguments, which gfx950 preloads into SGPRs (the library is built with -amdgpu-kernarg-preload-count): no wave waits
+// The single-round kernel with the 13-bit table (token path with BF16 x, or dequantization: MODE) with the inputs of
+// its first requests as leading scalar arguments, which gfx950 preloads into SGPRs (the library is built with
+// -amdgpu-kernarg-preload-count): no wave waits
 // for a kernarg read before requesting the table, header bytes, activations and streams (4B sweep 1685 -> 1644 us per
 // token).  The eight arguments fill the 14 SGPRs gfx950 preloads next to the kernarg pointer; the row index, whose
 // first use comes after the streams are in LDS, is read from `a`.  With fixed slots the stream copy needs only `data`
@@ -556,7 +557,7 @@ __device__ __forceinline__ void take_preloaded(BlockArgs &a, const uint8_t *data
     a.data = data; a.bases = bases; a.seq = seq; a.M = M; a.K = K; a.hdr = hdr; a.x = xp;
     a.stride = ((pk >> 22) & 0xFFu) * 16u;
 }
-template <int ELEM, int NR>
+template <int ELEM, int NR, int MODE = kToken>
 __global__ void __launch_bounds__(1024) k_layout0p(const uint8_t *__restrict__ data, const uint32_t *__restrict__ bases,
                                                    const uint32_t *__restrict__ seq, uint32_t M, uint32_t K, uint32_t pk,
                                                    const uint8_t *__restrict__ hdr, const void *__restrict__ xp,
@@ -565,8 +566,8 @@ __global__ void __launch_bounds__(1024) k_layout0p(const uint8_t *__restrict__ d
     extern __shared__ uint32_t dyn[];
     take_preloaded(a, data, bases, seq, M, K, pk, hdr, xp);
     a.G = pk & 0xFFFFu;
-    layout0_body<ELEM, kToken, true, false, NR, kPeekSeq>(a, ((pk >> 16) & 0x3Fu) * 32u, pk >> 30, blockIdx.x * a.G, 0u,
-                                                          s, dyn);
+    layout0_body<ELEM, MODE, true, false, NR, kPeekSeq>(a, ((pk >> 16) & 0x3Fu) * 32u, pk >> 30, blockIdx.x * a.G, 0u,
+                                                        s, dyn);
 }
 
 // Layout-0 token path and dequantization for matrices of one to two row groups per CU (k_layout0t): the first nfull
@@ -620,11 +621,11 @@ static int launch_layout0_tail(const LaunchPlan &p, const BlockArgs &a, hipStrea
     return (int)hipGetLastError();
 }
 
-template <int ELEM, int NR>
+template <int ELEM, int NR, int MODE = kToken>
 static void launch_layout0p(const LaunchPlan &p, const BlockArgs &a, hipStream_t st) {
     const uint32_t pk = p.G | ((p.threads / 32u) << 16) | ((a.stride >> 4) << 22) | (a.scale ? 1u << 30 : 0u) |
                         (a.bias ? 1u << 31 : 0u);
-    hipLaunchKernelGGL((k_layout0p<ELEM, NR>), dim3(p.grid), dim3(p.threads), p.lds, st, a.data, a.bases, a.seq,
+    hipLaunchKernelGGL((k_layout0p<ELEM, NR, MODE>), dim3(p.grid), dim3(p.threads), p.lds, st, a.data, a.bases, a.seq,
                        a.M, a.K, pk, a.hdr, a.x, a);
 }
 
@@ -1300,11 +1301,11 @@ static int launch_prefix_t(const LaunchPlan &p, const BlockArgs &a, hipStream_t 
     if constexpr ((MODE == kToken && XBF16) || MODE == kDequant) {
         if (p.layout == 0 && p.tail) return launch_layout0_tail<ELEM, MODE>(p, a, st);   // whole row groups + split tail
     }
-    if constexpr (MODE == kToken && XBF16) {
+    if constexpr ((MODE == kToken && XBF16) || MODE == kDequant) {
         if (p.layout == 0 && p.seq13 && !p.pipe && p.G < 65536u) {
-            if (p.split == 2) launch_layout0p<ELEM, 4>(p, a, st);
-            else if (p.split == 4) launch_layout0p<ELEM, 2>(p, a, st);
-            else launch_layout0p<ELEM, 8>(p, a, st);
+            if (p.split == 2) launch_layout0p<ELEM, 4, MODE>(p, a, st);
+            else if (p.split == 4) launch_layout0p<ELEM, 2, MODE>(p, a, st);
+            else launch_layout0p<ELEM, 8, MODE>(p, a, st);
             return (int)hipGetLastError();
         }
     }
