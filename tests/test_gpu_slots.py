@@ -90,3 +90,23 @@ def test_dequant_without_table_matches(cuda, monkeypatch):
         outs.append(out)
     _same(outs[0], outs[1], "nwc_dequant")
     _same(outs[0], c.dequant(), "nwc_dequant against nwc_dequant_seq")
+
+
+@pytest.mark.parametrize("layout,elem", [(0, "bf16"), (1, "bf16"), (0, "fp8")])
+def test_checkpoint_tensors_are_the_packed_encoding(cuda, layout, elem):
+    """A matrix placed on the GPU in fixed slots gives back, through tensors() (what save_pretrained writes), exactly
+    the tensors the same matrix has on the CPU, where it stays packed as the encoder wrote it."""
+    import nwc_amd.nwc_torch as N
+    w = bf16_matrix(2560, 4096, seed=11, escapes=elem != "fp8")
+    if elem == "fp8":
+        q, s = N.quantize_fp8(w.float())
+        g = N.NWCWeight(q, device="cuda:0", elem="fp8", scale=s, layout=layout)
+        h = N.NWCWeight(q, device="cpu", elem="fp8", scale=s, layout=layout)
+    else:
+        g = N.NWCWeight(w, device="cuda:0", layout=layout)
+        h = N.NWCWeight(w, device="cpu", layout=layout)
+    assert g._slot and not h._slot and g.bytes == h.bytes
+    tg, th = g.tensors(), h.tensors()
+    assert tg.keys() == th.keys()
+    for name in th:
+        assert torch.equal(tg[name].cpu(), th[name]), name
