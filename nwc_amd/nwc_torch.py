@@ -264,7 +264,9 @@ class NWCWeight:
         self.bytes_bf16 = 2 * self.n
         self.bytes_native = self.n + 4 * self.out_features if self.elem == ELEM_FP8 else 2 * self.n
         self._packed_len = self.data.numel()
-        if self.layout <= 1 and FIXED_SLOTS and self.data.device.type == "cuda" and self.bases.numel():
+        # (not inside HIP-graph capture: the move ends in a host read of two sums)
+        if (self.layout <= 1 and FIXED_SLOTS and self.data.device.type == "cuda" and self.bases.numel()
+                and not torch.cuda.is_current_stream_capturing()):
             self._to_slots()
 
     def _to_slots(self):
