@@ -140,7 +140,7 @@ __device__ __forceinline__ uint32_t matrix_end(const BlockArgs &a, uint32_t nb) 
 }
 
 // Blocks [b_lo, b_hi) plus the 16 bytes the last lane's window reads past its stream (inside the 64 slack bytes that
-// follow the matrix's last block, or the 128 after its last slot).  stride: a.stride for layout 0, 0 for layout 1.
+// follow the matrix's last block, or the 128 after its last slot).  stride: a.stride (fixed slots) or 0 (bases[]).
 __device__ __forceinline__ Region region_of(const BlockArgs &a, uint32_t b_lo, uint32_t b_hi, uint32_t nb, uint32_t mend,
                                             uint32_t stride) {
     Region r;
@@ -430,8 +430,9 @@ __device__ __forceinline__ void layout0_body(BlockArgs a, uint32_t nth, uint32_t
     const uint32_t nt = ng * f.CB, tl = nt - 1u;              // look-ahead past the tile re-reads block tl
     const uint32_t B0 = rg0 * f.CB, nb = f.nb;
     const uint32_t mend = !a.stride && B0 + nt == nb ? matrix_end(a, nb) : 0u;
-    // request order: region bounds and table first, then the stream copy (which needs the bounds), then the raw rows
-    // and activations; loads complete in order, so each wait below covers only what it needs
+    // request order: region bounds (none with fixed slots) and table first, then the stream copy (which needs the
+    // bounds), then the activations and the raw rows; loads complete in order, so each wait below covers only what it
+    // needs
     uint32_t t = hw / SP;
     const uint32_t r0 = PART ? NR * jfix : (hw % SP) * NR;    // first row of this half-wave's share of the block
     Coord0 c = coord0(min(t, tl), rg0, f, L);
@@ -544,9 +545,8 @@ __global__ void __launch_bounds__(1024) k_layout0(BlockArgs a) {
 
 // The single-round kernel with the 13-bit table (token path with BF16 x, or dequantization: MODE) with the inputs of
 // its first requests as leading scalar arguments, which gfx950 preloads into SGPRs (the library is built with
-// -amdgpu-kernarg-preload-count): no wave waits
-// for a kernarg read before requesting the table, header bytes, activations and streams (4B sweep 1685 -> 1644 us per
-// token).  The eight arguments fill the 14 SGPRs gfx950 preloads next to the kernarg pointer; the row index, whose
+// -amdgpu-kernarg-preload-count): no wave waits for a kernarg read before requesting the table, header bytes,
+// activations and streams (4B sweep 1685 -> 1644 us per token).  The eight arguments fill the 14 SGPRs gfx950 preloads next to the kernarg pointer; the row index, whose
 // first use comes after the streams are in LDS, is read from `a`.  With fixed slots the stream copy needs only `data`
 // and pk; otherwise it waits for the region bounds read from `bases`.
 // pk = G | H << 16 | stride / 16 << 22 | has_scale << 30 | has_bias << 31, H = the workgroup's half-waves (at most
