@@ -42,7 +42,7 @@ SEQ_TABLE = os.environ.get("NWC_SEQ_TABLE", "1") != "0"   # layouts 0/1: stage t
 # offset instead of reading it before they can request the streams (Qwen3-4B layout-0 sweep 1577 -> 1523 us per token)
 FIXED_SLOTS = os.environ.get("NWC_FIXED_SLOTS", "1") != "0"
 SLOT_MAX = {0: 1728, 1: 3040}     # the library's largest stride per layout (nwc_format.h kSlotMax0 / kSlotMax1)
-SLOT_OVERHEAD = 1.06              # slots only where they hold at most 6% more bytes than the packed streams
+SLOT_OVERHEAD = 1.15              # slots only where they hold at most 15% more bytes than the packed streams
 SLOT_TAIL = 2 * DATA_SLACK        # zero bytes after the last slot (the packed form keeps 64 + DATA_SLACK)
 ROW_INDEX = os.environ.get("NWC_ROW_INDEX", "1") != "0"   # layouts 0/1: build the row index for the token path
 # layout 0: inputs of 2..BATCH_MAX tokens go through the fused kernel (four vectors per launch) instead of a

@@ -30,8 +30,8 @@ SHAPES = [
 
 def _twins(M, K, elem, monkeypatch, layout=0):
     import nwc_amd.nwc_torch as N
-    # fp8 without the 1e30 stressors: a row holding one quantizes to zeros, and such short row groups would keep
-    # the matrix packed (the slots would hold more than 6% padding)
+    # fp8 without the 1e30 stressors: a row holding one quantizes to zeros, and the spread of block sizes that such
+    # row groups add can keep a matrix packed (2560x9728 would need a 1744-byte stride, past the largest)
     w = bf16_matrix(M, K, seed=M + K, escapes=elem != "fp8")
     if elem == "fp8":
         q, s = N.quantize_fp8(w.float())
