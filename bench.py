@@ -433,13 +433,14 @@ def run_stream_ceiling(args, sizes_mb=(14.5, 21.8, 34.1, 68.0), copies=36):
 
 
 def run_prefill(args):
-    """configs[2] prefill: per 4B matrix, dequantization into a BF16 buffer + the hipBLASLt GEMM of --prefill tokens,
-    against the same GEMM on resident BF16 weights, and (layout 0) the fused prefill kernel without the buffer
-    (nwc_prefill_xbf16, checked against float64 to the fp32-accumulation bound); 8 copies rotate so every launch
-    reads HBM."""
+    """configs[2] prefill: per 4B matrix, dequantization into a BF16 buffer + the GEMM of --prefill tokens that
+    NWCLinear runs (linear_dequantized: hipBLASLt, or the library's split-K GEMM on the shapes where that measured
+    faster), against hipBLASLt on resident BF16 weights (the uncompressed model) and the same GEMM choice on them,
+    and (layout 0) the fused prefill kernel without the buffer (nwc_prefill_xbf16, checked against float64 to the
+    fp32-accumulation bound); 8 copies rotate so every launch reads HBM."""
     import torch
     import torch.nn.functional as F
-    from nwc_amd.nwc_torch import NWCWeight
+    from nwc_amd.nwc_torch import NWCWeight, linear_dequantized
     torch.backends.cuda.preferred_blas_library("hipblaslt")
     dev = torch.device("cuda:0")
     T, R = args.prefill, 8
@@ -451,14 +452,21 @@ def run_prefill(args):
         wb = [w.to(dev) for _ in range(R)]
         tmp = torch.empty(M, c.K16, dtype=torch.bfloat16, device=dev)
         x = torch.randn(T, K, generator=torch.Generator().manual_seed(3000 + si)).to(torch.bfloat16).to(dev)
-        y = F.linear(x, cs[R - 1].dequant(tmp)[:, :K])
-        ref = F.linear(x, wb[0])
+        y = linear_dequantized(x, cs[R - 1].dequant(tmp)[:, :K])
+        ref = linear_dequantized(x, wb[0])
         if not torch.equal(y, ref):                 # same BF16 weights, same GEMM: identical outputs
             raise SystemExit(f"{name}: prefill through the compressed weights differs from the resident GEMM")
+        refd = x.double() @ wb[0].double().t()
+        bound = 2.0 ** -8 * refd.abs() + 2.0 ** -20 * (x.double().abs() @ wb[0].double().abs().t()) + 1e-6
+        if ((y.double() - refd).abs() > bound).any():
+            raise SystemExit(f"{name}: prefill GEMM outside the fp32-accumulation bound of float64")
+        del refd, bound
         modes = [("dequant", [(lambda j=j: cs[j].dequant(tmp)) for j in range(R)]),
-                 ("gemm", [(lambda j=j: F.linear(x, tmp[:, :K])) for j in range(R)]),
-                 ("dequant_gemm", [(lambda j=j: F.linear(x, cs[j].dequant(tmp)[:, :K])) for j in range(R)]),
-                 ("resident_bf16", [(lambda j=j: F.linear(x, wb[j])) for j in range(R)])]
+                 ("gemm", [(lambda j=j: linear_dequantized(x, tmp[:, :K])) for j in range(R)]),
+                 ("dequant_gemm", [(lambda j=j: linear_dequantized(x, cs[j].dequant(tmp)[:, :K])) for j in range(R)]),
+                 ("dequant_hipblaslt", [(lambda j=j: F.linear(x, cs[j].dequant(tmp)[:, :K])) for j in range(R)]),
+                 ("resident_bf16", [(lambda j=j: F.linear(x, wb[j])) for j in range(R)]),
+                 ("resident_same_gemm", [(lambda j=j: linear_dequantized(x, wb[j])) for j in range(R)])]
         if args.layout == 0:
             yf = cs[R - 1].prefill(x, None).double()
             refd = x.double() @ w.to(dev).double().t()
@@ -478,9 +486,10 @@ def run_prefill(args):
                      "gemm_TFLOPs": round(2 * T * M * K / (t["gemm"] * 1e-6) / 1e12, 1)})
         del cs, wb, tmp
         torch.cuda.empty_cache()
-    keys = ("dequant_us", "gemm_us", "dequant_gemm_us", "resident_bf16_us") + (("fused_us",) if args.layout == 0 else ())
+    keys = ("dequant_us", "gemm_us", "dequant_gemm_us", "dequant_hipblaslt_us", "resident_bf16_us",
+            "resident_same_gemm_us") + (("fused_us",) if args.layout == 0 else ())
     tot = {k: round(LAYERS * sum(r[k] for r in rows), 1) for k in keys}
-    return {"metric": f"{args.prefill}-token prefill per Qwen3-4B stack: dequant to BF16 + hipBLASLt GEMM vs resident BF16 GEMM",
+    return {"metric": f"{args.prefill}-token prefill per Qwen3-4B stack: dequant to BF16 + GEMM vs resident BF16 GEMM",
             "value": tot["dequant_gemm_us"], "unit": "us", "higher_is_better": False, "dtype": "bf16",
             "config": {"workload": "Qwen3-4B-shaped prefill (BASELINE configs[2]), 36 layers", "layout": args.layout,
                        "tokens": T},

@@ -154,6 +154,21 @@ int nwc_ref_fp8(void *stream, const uint8_t *w, const float *scale, const float 
  * BF16 [K], y BF16 [M], fp32 accumulation.  No counterpart in the reference (its BF16 bar is cuBLAS through F.linear). */
 int nwc_ref_bf16(void *stream, const uint16_t *w, const uint16_t *x, uint16_t *y, uint64_t M, uint32_t K);
 
+/* Bytes of workspace nwc_gemm_xbf16 needs for this product on the current device (0: none). */
+uint64_t nwc_gemm_workspace(uint32_t T, uint32_t N, uint32_t K);
+
+/* Prefill product of a dequantized matrix: y[t][n] = RNE_bf16(sum_k x[t][k] w[n][k] + bias[n]) for t < T, n < N;
+ * x BF16 [T x K] with row stride ldx, w BF16 [N x K] with row stride ldw (nwc_dequant_seq's output, ldw = K16), bias
+ * BF16 [N] or null, y BF16 [T x N] row-major; fp32 accumulation on the matrix cores.  K a multiple of 64, ldx and
+ * ldw multiples of 8, x and w 16-byte aligned, y 8-byte aligned.  When nwc_gemm_workspace(T, N, K) > 0 the columns
+ * are split over several workgroups per output tile: `ws` (256-byte aligned, ws_bytes at least that) holds their
+ * partial sums, and its first 4096 bytes are counters that must be zero before the first call on a buffer (every
+ * call leaves them zero).  Calls that share a workspace must not overlap (order them on one stream).  The partial
+ * sums are added in a fixed order, so a call's result does not depend on the timing.  Replaces the cuBLAS GEMM of
+ * the reference's prefill (nwc/nwc_torch.py:320-323: F.linear on the dequantized matrix); no ABI counterpart. */
+int nwc_gemm_xbf16(void *stream, const uint16_t *x, uint32_t ldx, const uint16_t *w, uint32_t ldw,
+                   const uint16_t *bias, uint16_t *y, uint32_t T, uint32_t N, uint32_t K, void *ws, uint64_t ws_bytes);
+
 /* Measurement kernel: `grid` workgroups read p[0 .. bytes) once (16-byte non-temporal loads, bytes a multiple of 16,
  * p 16-byte aligned) and write one folded word each to out[0 .. grid).  The read bandwidth a launch of that size
  * reaches.  No counterpart in the reference. */

@@ -35,6 +35,8 @@ SIGNATURES = {
     "nwc_gather": ("i", "pppppppIpQIIi"),
     "nwc_ref_fp8": ("i", "pppppQI"),
     "nwc_ref_bf16": ("i", "ppppQI"),
+    "nwc_gemm_workspace": ("Q", "III"),
+    "nwc_gemm_xbf16": ("i", "ppIpIppIIIpQ"),
     "nwc_stream_read": ("i", "ppQpI"),
     "nwc_setup": ("i", ""),
 }

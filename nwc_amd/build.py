@@ -19,7 +19,7 @@ CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 TARGET_DIR = os.path.join(HERE, "lib")
 TARGET = os.path.join(TARGET_DIR, "nwc_ops.so")
-SOURCES = ["encode.cpp", "abi.cpp", "kern_prefix.hip", "kern_fixed.hip", "kern_misc.hip"]
+SOURCES = ["encode.cpp", "abi.cpp", "kern_prefix.hip", "kern_fixed.hip", "kern_misc.hip", "kern_gemm.hip"]
 # -packed-fp32-ops: no v_pk_*_f32 anywhere (hipcc's host pass warns that it does not know the feature)
 # -amdgpu-kernarg-preload-count: gfx950 loads a kernel's leading scalar arguments into SGPRs before its first
 # instruction (kernels that take them, k_layout0p); kernels whose first argument is a struct keep reading theirs

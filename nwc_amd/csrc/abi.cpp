@@ -406,6 +406,26 @@ extern "C" int nwc_ref_bf16(void *stream, const uint16_t *w, const uint16_t *x, 
     return launch_ref_bf16(w, x, y, (uint32_t)M, K, ncu, (hipStream_t)stream);
 }
 
+extern "C" uint64_t nwc_gemm_workspace(uint32_t T, uint32_t N, uint32_t K) {
+    const int ncu = current_cus();
+    return ncu > 0 ? gemm_workspace_bytes(T, N, K, ncu) : 0;
+}
+
+extern "C" int nwc_gemm_xbf16(void *stream, const uint16_t *x, uint32_t ldx, const uint16_t *w, uint32_t ldw,
+                              const uint16_t *bias, uint16_t *y, uint32_t T, uint32_t N, uint32_t K, void *ws,
+                              uint64_t ws_bytes) {
+    if (T == 0 || N == 0 || K == 0 || K % 64u != 0 || ldx < K || ldw < K || ldx % 8u != 0 || ldw % 8u != 0 ||
+        ((uintptr_t)x & 15u) != 0 || ((uintptr_t)w & 15u) != 0 || ((uintptr_t)y & 7u) != 0 ||
+        ((uintptr_t)bias & 1u) != 0 || (uint64_t)T * N >= (1ull << 32))
+        return -1;
+    const int ncu = current_cus();
+    if (ncu <= 0) return (int)hipErrorNoDevice;
+    const uint64_t need = gemm_workspace_bytes(T, N, K, ncu);
+    if (need && (ws == nullptr || ws_bytes < need || ((uintptr_t)ws & 255u) != 0)) return -1;
+    GemmArgs g{x, w, bias, y, nullptr, nullptr, ldx, ldw, T, N, K, 0, 0, 0};
+    return launch_gemm_xwt(g, ws, ncu, (hipStream_t)stream);
+}
+
 extern "C" int nwc_stream_read(void *stream, const void *p, uint64_t bytes, uint32_t *out, uint32_t grid) {
     if (bytes == 0 || bytes % 16 != 0 || ((uintptr_t)p & 15u) != 0 || grid == 0) return -1;
     if (current_cus() <= 0) return (int)hipErrorNoDevice;

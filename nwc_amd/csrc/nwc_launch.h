@@ -2,6 +2,8 @@
 #pragma once
 #include "nwc_device.h"
 
+#include <algorithm>
+
 namespace nwc {
 
 struct LaunchPlan {
@@ -25,6 +27,18 @@ int launch_layout0_batch(const LaunchPlan &p, int elem_t, const BlockArgs &a, ui
 int launch_gather_fixed(int elem_t, const GatherArgs &a, hipStream_t st);
 // layout-0 prefill (k_prefill0): tt tokens per workgroup tile (64, 128, 256 or 512)
 int launch_prefill0(int elem_t, uint32_t tt, const PrefillArgs &p, hipStream_t st);
+// Y[T x N] = X[T x K] W[N x K]^T (+ bias), BF16 (k_gemm_xwt); the launcher fills nT, S, stages, cnt and part
+struct GemmArgs {
+    const uint16_t *x, *w, *bias;
+    uint16_t *y;
+    float *part;            // S partial tiles per output tile (split products)
+    uint32_t *cnt;          // per output tile: workgroups of its splits that have finished
+    uint32_t ldx, ldw, T, N, K, nT, S, stages;
+};
+constexpr uint32_t kGemmCounters = 1024;
+uint32_t gemm_splits(uint32_t T, uint32_t N, uint32_t K, int ncu);
+uint64_t gemm_workspace_bytes(uint32_t T, uint32_t N, uint32_t K, int ncu);
+int launch_gemm_xwt(GemmArgs g, void *ws, int ncu, hipStream_t st);
 int launch_ref_fp8(const uint8_t *w, const float *scale, const float *x, uint16_t *y, uint32_t M, uint32_t K, int ncu,
                    hipStream_t st);
 int launch_ref_bf16(const uint16_t *w, const uint16_t *x, uint16_t *y, uint32_t M, uint32_t K, int ncu, hipStream_t st);

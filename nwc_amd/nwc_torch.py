@@ -53,6 +53,10 @@ BATCH_LAUNCH = 4                                           # vectors per nwc_lin
 # "fused" runs nwc_prefill_xbf16 (decode into LDS + matrix cores, no temporary matrix; correct, but slower on MI355X
 # at 512 tokens: 20 ms against 8.5 ms per Qwen3-4B stack)
 PREFILL = os.environ.get("NWC_PREFILL", "dequant")
+# the prefill GEMM on the temporary matrix: "auto" (default) the library's split-K matrix-core kernel
+# (nwc_gemm_xbf16) for the shapes where it measured faster than hipBLASLt on MI355X, torch's F.linear for the rest;
+# "nwc" the library kernel wherever it applies; "hipblaslt" F.linear always
+GEMM = os.environ.get("NWC_GEMM", "auto")
 FP8_MAX = 448.0
 
 
@@ -107,6 +111,67 @@ def ref_bf16_matvec(w: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
     wc, xc = w.contiguous(), x.to(torch.bfloat16).contiguous()
     call("nwc_ref_bf16", stream(), ptr(wc), ptr(xc), ptr(y), rows, cols)
     return y
+
+
+# device index -> workspace of nwc_gemm_xbf16 (its counters are zero between calls).  Calls on one device share it,
+# so they must not run concurrently on two streams.  A workspace that a larger one replaces stays allocated: graphs
+# captured earlier keep its address.
+_GEMM_WS = {}
+_GEMM_WS_RETIRED = []
+
+
+def gemm_usable(x: torch.Tensor, weight: torch.Tensor) -> bool:
+    """Whether gemm_xbf16 takes this product: BF16 on the GPU, K a multiple of 64, rows of 16-byte multiples."""
+    return (x.dtype == torch.bfloat16 and weight.dtype == torch.bfloat16 and x.is_cuda
+            and weight.dim() == 2 and weight.shape[1] % 64 == 0 and weight.stride(1) == 1
+            and weight.stride(0) % 8 == 0 and weight.data_ptr() % 16 == 0)
+
+
+def gemm_preferred(tokens: int, out_features: int, in_features: int) -> bool:
+    """Where nwc_gemm_xbf16 beats hipBLASLt on MI355X (graph-timed against F.linear, 16-2048 tokens on the Qwen3-4B
+    projection shapes): K of 8192 or more at 128-768 tokens (the down projection, 2560 x 9728: 1.08-1.70x), where the
+    output has few 128 x 128 tiles and the split over K fills the CUs.  Everywhere else hipBLASLt was faster."""
+    return in_features >= 8192 and 128 <= tokens <= 768
+
+
+def linear_dequantized(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor = None) -> torch.Tensor:
+    """The prefill product on a dequantized matrix, F.linear(x, weight, bias): the library GEMM (gemm_xbf16) where
+    NWC_GEMM and gemm_preferred choose it, torch's F.linear (hipBLASLt) otherwise.  The choice depends on the shapes
+    only, so a dequantized matrix and the same matrix resident in BF16 go through the same GEMM."""
+    if gemm_usable(x, weight) and (GEMM == "nwc" or (GEMM == "auto" and gemm_preferred(
+            x.numel() // weight.shape[1], weight.shape[0], weight.shape[1]))):
+        return gemm_xbf16(x, weight, bias)
+    return F.linear(x, weight, bias)
+
+
+def gemm_xbf16(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor = None) -> torch.Tensor:
+    """F.linear(x, weight, bias) in BF16 through the library's split-K matrix-core GEMM (nwc_gemm_xbf16): x [..., K],
+    weight [N, K] (a row-strided view such as dequant()'s is fine), bias [N] or None; fp32 accumulation, one RNE
+    rounding of the sum + bias.  The partial sums are added in a fixed order: equal inputs give equal bits."""
+    _need_gpu(weight)
+    N, K = weight.shape
+    xs = x.reshape(-1, K)
+    if xs.stride(-1) != 1 or xs.stride(0) % 8 or xs.data_ptr() % 16:
+        xs = xs.contiguous()
+    T = xs.shape[0]
+    y = torch.empty(T, N, dtype=torch.bfloat16, device=weight.device)
+    if T == 0:
+        return y.view(*x.shape[:-1], N)
+    need = int(lib.nwc_gemm_workspace(T, N, K))
+    ws = None
+    if need:
+        key = weight.device.index
+        ws = _GEMM_WS.get(key)
+        if ws is None or ws.numel() < need:
+            if torch.cuda.is_current_stream_capturing():
+                raise RuntimeError("gemm_xbf16: run this shape once outside graph capture first (workspace)")
+            if ws is not None:
+                _GEMM_WS_RETIRED.append(ws)
+            ws = _GEMM_WS[key] = torch.zeros(need, dtype=torch.uint8, device=weight.device)
+    b = None if bias is None else bias.to(torch.bfloat16).contiguous()
+    call("nwc_gemm_xbf16", stream(), ptr(xs), xs.stride(0), ptr(weight), weight.stride(0), ptr(b), ptr(y), T, N, K,
+         ptr(ws), 0 if ws is None else ws.numel())
+    return y.view(*x.shape[:-1], N)
 
 
 def fits(out_features, in_features):
@@ -528,8 +593,9 @@ def _bf16_bias(bias, device):
 class NWCLinear(nn.Module):
     """nn.Linear over a compressed matrix (elem "bf16" lossless, or "fp8" weight-only).  One BF16 token goes through
     the fused decode-matvec kernel, up to NWC_BATCH_MAX (8) BF16 tokens of a layout-0 matrix through the batched one
-    (the matrix decoded once per four tokens); anything else through a temporary BF16 matrix and F.linear, or, with
-    NWC_PREFILL=fused, BF16 tokens of a layout-0 matrix through the fused prefill kernel (NWCWeight.prefill)."""
+    (the matrix decoded once per four tokens); anything else through a temporary BF16 matrix and linear_dequantized
+    (hipBLASLt, or the library's split-K GEMM where that is faster), or, with NWC_PREFILL=fused, BF16 tokens of a
+    layout-0 matrix through the fused prefill kernel (NWCWeight.prefill)."""
 
     def __init__(self, linear: nn.Linear = None, device="cuda", block=None, w: "NWCWeight" = None, bias=None,
                  elem="bf16"):
@@ -557,9 +623,9 @@ class NWCLinear(nn.Module):
             return y.view(*x.shape[:-1], self.out_features)
         weight = self.w.dequant()
         if self.w.scale is None:
-            return F.linear(x, weight, self.bias)
+            return linear_dequantized(x, weight, self._bias_data())
         # fp8: the product of the unscaled codes, then the row scale and the bias in fp32
-        y = F.linear(x, weight).float() * self.w.scale
+        y = linear_dequantized(x, weight).float() * self.w.scale
         if self.bias is not None:
             y = y + self.bias.float()
         return y.to(x.dtype)

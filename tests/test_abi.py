@@ -14,10 +14,19 @@ REFERENCE_EXPORTS = {"nwc_info", "nwc_layout", "nwc_encode", "nwc_build_tab", "n
                      "nwc_linear_bf16", "nwc_gather", "nwc_ref_fp8", "nwc_setup"}      # nwc_ops.cu:27-39
 
 
-def _declared():
+def _declarations():
+    """name -> number of parameters, for every function include/nwc_ops.h declares"""
     text = open(HEADER).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return set(re.findall(r"^\s*(?:int|int64_t|void)\s+(nwc_\w+)\s*\(", text, flags=re.M))
+    out = {}
+    for name, params in re.findall(r"^\s*(?:int|int64_t|uint64_t|void)\s+(nwc_\w+)\s*\(([^)]*)\)", text, flags=re.M):
+        params = params.strip()
+        out[name] = 0 if params in ("", "void") else params.count(",") + 1
+    return out
+
+
+def _declared():
+    return set(_declarations())
 
 
 def _lib():
@@ -30,7 +39,17 @@ def test_header_declares_the_reference_exports():
     assert REFERENCE_EXPORTS <= d
     assert d - REFERENCE_EXPORTS == {"nwc_linear_xbf16", "nwc_linear_xbf16_batch", "nwc_row_index", "nwc_token_split",
                                      "nwc_seq_table", "nwc_dequant_seq", "nwc_prefill_xbf16",
-                                     "nwc_gather_xindex", "nwc_ref_bf16", "nwc_stream_read"}              # this build's additions
+                                     "nwc_gather_xindex", "nwc_ref_bf16", "nwc_stream_read", "nwc_gemm_workspace",
+                                     "nwc_gemm_xbf16"}              # this build's additions
+
+
+def test_binding_signatures_match_the_header():
+    """The ctypes table (nwc_amd/_abi.py) declares every header function with the header's number of arguments."""
+    from nwc_amd._abi import SIGNATURES
+    decl = _declarations()
+    assert set(SIGNATURES) == set(decl)
+    for name, (_, args) in SIGNATURES.items():
+        assert len(args) == decl[name], name
 
 
 def test_library_exports_every_declared_symbol():

@@ -10,7 +10,7 @@ and the reference's own token entry point nwc_linear_bf16, bound with the refere
 
 Bars: decoded weights and gathered rows bit-exact against the original weights (and, for configs[0], against the
 oracle's decode of the same tensors); token path rounded to nearest even from within 1e-3 |y| + 1e-5 of a float64
-matvec on the decoded weights (RNE(y64 - tol) <= y <= RNE(y64 + tol)); fp32 path within 1e-3 |y| + 1e-5; prefill equal to F.linear on the original BF16 weights (the same
+matvec on the decoded weights (RNE(y64 - tol) <= y <= RNE(y64 + tol)); fp32 path within 1e-3 |y| + 1e-5; prefill equal to the same GEMM on the original BF16 weights (the same
 GEMM on bit-identical operands)."""
 import ctypes
 
@@ -104,7 +104,9 @@ def test_config1_qwen3_06b_matrices(cuda, name):
 @pytest.mark.parametrize("layout", [0, 1])
 @pytest.mark.parametrize("name", list(QWEN3_4B))
 def test_config2_prefill_512(cuda, name, layout):
-    """a 512-token prefill (dequantization + hipBLASLt) equals the GEMM on the resident BF16 weights."""
+    """a 512-token prefill (dequantization + the GEMM NWCLinear picks for the shape) equals the same GEMM
+    on the resident BF16 weights."""
+    from nwc_amd.nwc_torch import linear_dequantized
     NWCWeight, NWCLinear, _ = _nwc()
     M, K = QWEN3_4B[name]
     print(f"configs[2] prefill 512 {name} {M}x{K} layout {layout}", flush=True)
@@ -113,7 +115,7 @@ def test_config2_prefill_512(cuda, name, layout):
     g = torch.Generator().manual_seed(11)
     x = torch.randn(1, 512, K, generator=g).to(torch.bfloat16).cuda()
     torch.backends.cuda.preferred_blas_library("hipblaslt")
-    assert torch.equal(lin(x), F.linear(x, w.cuda()))
+    assert torch.equal(lin(x), linear_dequantized(x, w.cuda()))
     check_token(lin(x[:, :1]).view(-1), y_exact(w.cuda(), x[0, 0].float().cpu()))
 
 
