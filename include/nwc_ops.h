@@ -4,17 +4,19 @@
  * docs/format.md:176-188): the same symbol names, argument order, argument meaning and return codes, so the
  * reference's ctypes bindings (nwc/nwc_torch.py:58-77) load this library unchanged.  Every pointer is a plain
  * address; `stream` is a hipStream_t passed as void* (torch.cuda.current_stream().cuda_stream), work is ordered on
- * it and no entry point synchronises the host.  The library allocates no device memory: outputs and the scratch
- * buffer belong to the caller.  `elem` = element type (0 BF16, 1 fp8 e4m3fn) | layout << 4 (layouts 0, 1, 2).
+ * it and no entry point synchronises the host.  The library allocates no device memory: outputs, the scratch
+ * buffer and workspaces belong to the caller.  `elem` = element type (0 BF16, 1 fp8 e4m3fn) | layout << 4 (layouts
+ * 0, 1, 2).
  * `block` must be 4096 (nwc_info(4)); K is the number of columns, n = M * K.
  *
  * This build's extension of `elem` (no counterpart in the reference, whose callers leave these bits zero): bits
- * 8-15 = S / 16 for a layout-0 matrix whose block streams sit in fixed slots of S bytes (16 <= S <= 1728, a
- * multiple of 16): block b's lane streams start at byte b * S of `data`, bases[b] == b * S, and `data` holds
- * nb * S + 128 bytes (the slots' padding and the tail zero).  Such tensors are still a valid tensor set of the
- * format; the bits only let the token kernels compute a block's offset instead of reading bases[b] before they can
- * request its streams.  A caller that sets them for tensors that do not meet this contract makes the kernels read
- * the wrong bytes.  The bits are refused (-1) for layouts 1/2, for S > 1728, or when nb * S + 128 >= 2^32.
+ * 8-15 = S / 16 for a layout-0 or layout-1 matrix whose block streams sit in fixed slots of S bytes (a multiple of
+ * 16, 16 <= S <= 1728 for layout 0 and <= 3040 for layout 1): block b's lane streams start at byte b * S of `data`,
+ * bases[b] == b * S, and `data` holds nb * S + 128 bytes (the slots' padding and the tail zero).  Such tensors are
+ * still a valid tensor set of the format; the bits only let the token kernels compute a block's offset instead of
+ * reading bases[b] before they can request its streams.  A caller that sets them for tensors that do not meet this
+ * contract makes the kernels read the wrong bytes.  The bits are refused (-1) for layout 2, for S above the layout's
+ * limit, or when nb * S + 128 >= 2^32.
  *
  * Device entry points return 0, -1 for a shape the format cannot describe (or, in this build, a raw plane the
  * kernels cannot address with 32-bit offsets: layout 0 with Mp * K16 >= 2^32 for Mp = M rounded up to 8 rows,
