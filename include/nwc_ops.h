@@ -5,8 +5,8 @@
  * reference's ctypes bindings (nwc/nwc_torch.py:58-77) load this library unchanged.  Every pointer is a plain
  * address; `stream` is a hipStream_t passed as void* (torch.cuda.current_stream().cuda_stream), work is ordered on
  * it and no entry point synchronises the host.  The library allocates no device memory: outputs, the scratch
- * buffer and workspaces belong to the caller.  `elem` = element type (0 BF16, 1 fp8 e4m3fn) | layout << 4 (layouts
- * 0, 1, 2).
+ * buffer and workspaces belong to the caller (nwc_gemm_xbf16_noalloc uses a static array of the library instead).
+ * `elem` = element type (0 BF16, 1 fp8 e4m3fn) | layout << 4 (layouts 0, 1, 2).
  * `block` must be 4096 (nwc_info(4)); K is the number of columns, n = M * K.
  *
  * This build's extension of `elem` (no counterpart in the reference, whose callers leave these bits zero): bits
@@ -170,6 +170,15 @@ uint64_t nwc_gemm_workspace(uint32_t T, uint32_t N, uint32_t K);
  * the reference's prefill (nwc/nwc_torch.py:320-323: F.linear on the dequantized matrix); no ABI counterpart. */
 int nwc_gemm_xbf16(void *stream, const uint16_t *x, uint32_t ldx, const uint16_t *w, uint32_t ldw,
                    const uint16_t *bias, uint16_t *y, uint32_t T, uint32_t N, uint32_t K, void *ws, uint64_t ws_bytes);
+
+/* nwc_gemm_xbf16 without the workspace arguments, for callers that cannot allocate device memory (code under graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc); no counterpart in the reference.  The partial sums
+ * live in a static array of the library, 24 MiB on each GPU it runs on, held until the process ends (its counters
+ * are cleared by a small kernel on `stream` at the first call on a device).  A product whose workspace would exceed
+ * 24 MiB returns -1.  Every call on one GPU shares that array, so calls that overlap on one GPU (two streams) race.
+ * Allocates nothing; same results as nwc_gemm_xbf16. */
+int nwc_gemm_xbf16_noalloc(void *stream, const uint16_t *x, uint32_t ldx, const uint16_t *w, uint32_t ldw,
+                           const uint16_t *bias, uint16_t *y, uint32_t T, uint32_t N, uint32_t K);
 
 /* Measurement kernel: `grid` workgroups read p[0 .. bytes) once (16-byte non-temporal loads, bytes a multiple of 16,
  * p 16-byte aligned) and write one folded word each to out[0 .. grid).  The read bandwidth a launch of that size

@@ -37,6 +37,7 @@ SIGNATURES = {
     "nwc_ref_bf16": ("i", "ppppQI"),
     "nwc_gemm_workspace": ("Q", "III"),
     "nwc_gemm_xbf16": ("i", "ppIpIppIIIpQ"),
+    "nwc_gemm_xbf16_noalloc": ("i", "ppIpIppIII"),
     "nwc_stream_read": ("i", "ppQpI"),
     "nwc_setup": ("i", ""),
 }

@@ -411,17 +411,40 @@ extern "C" uint64_t nwc_gemm_workspace(uint32_t T, uint32_t N, uint32_t K) {
     return ncu > 0 ? gemm_workspace_bytes(T, N, K, ncu) : 0;
 }
 
+namespace {
+bool gemm_args_ok(const uint16_t *x, uint32_t ldx, const uint16_t *w, uint32_t ldw, const uint16_t *bias,
+                  const uint16_t *y, uint32_t T, uint32_t N, uint32_t K) {
+    return !(T == 0 || N == 0 || K == 0 || K % 64u != 0 || ldx < K || ldw < K || ldx % 8u != 0 || ldw % 8u != 0 ||
+             ((uintptr_t)x & 15u) != 0 || ((uintptr_t)w & 15u) != 0 || ((uintptr_t)y & 7u) != 0 ||
+             ((uintptr_t)bias & 1u) != 0 || (uint64_t)T * N >= (1ull << 32));
+}
+}  // namespace
+
 extern "C" int nwc_gemm_xbf16(void *stream, const uint16_t *x, uint32_t ldx, const uint16_t *w, uint32_t ldw,
                               const uint16_t *bias, uint16_t *y, uint32_t T, uint32_t N, uint32_t K, void *ws,
                               uint64_t ws_bytes) {
-    if (T == 0 || N == 0 || K == 0 || K % 64u != 0 || ldx < K || ldw < K || ldx % 8u != 0 || ldw % 8u != 0 ||
-        ((uintptr_t)x & 15u) != 0 || ((uintptr_t)w & 15u) != 0 || ((uintptr_t)y & 7u) != 0 ||
-        ((uintptr_t)bias & 1u) != 0 || (uint64_t)T * N >= (1ull << 32))
-        return -1;
+    if (!gemm_args_ok(x, ldx, w, ldw, bias, y, T, N, K)) return -1;
     const int ncu = current_cus();
     if (ncu <= 0) return (int)hipErrorNoDevice;
     const uint64_t need = gemm_workspace_bytes(T, N, K, ncu);
     if (need && (ws == nullptr || ws_bytes < need || ((uintptr_t)ws & 255u) != 0)) return -1;
+    GemmArgs g{x, w, bias, y, nullptr, nullptr, ldx, ldw, T, N, K, 0, 0, 0};
+    return launch_gemm_xwt(g, ws, ncu, (hipStream_t)stream);
+}
+
+extern "C" int nwc_gemm_xbf16_noalloc(void *stream, const uint16_t *x, uint32_t ldx, const uint16_t *w, uint32_t ldw,
+                                      const uint16_t *bias, uint16_t *y, uint32_t T, uint32_t N, uint32_t K) {
+    if (!gemm_args_ok(x, ldx, w, ldw, bias, y, T, N, K)) return -1;
+    const int ncu = current_cus();
+    if (ncu <= 0) return (int)hipErrorNoDevice;
+    const uint64_t need = gemm_workspace_bytes(T, N, K, ncu);
+    if (need > kGemmScratchBytes) return -1;
+    void *ws = nullptr;
+    if (need) {
+        int err = 0;
+        ws = gemm_scratch((hipStream_t)stream, &err);
+        if (ws == nullptr) return err ? err : (int)hipErrorInvalidValue;
+    }
     GemmArgs g{x, w, bias, y, nullptr, nullptr, ldx, ldw, T, N, K, 0, 0, 0};
     return launch_gemm_xwt(g, ws, ncu, (hipStream_t)stream);
 }

@@ -7,7 +7,13 @@
 // a few hundred tokens: the down projection); hipBLASLt stays faster on the others.
 #include "nwc_launch.h"
 
+#include <mutex>
+
 namespace nwc {
+
+// Workspace of nwc_gemm_xbf16_noalloc, for callers that cannot allocate: one copy per GPU, held until the process
+// ends.  Host code uses the address hipGetSymbolAddress gives for the current device, never this name.
+static __device__ __attribute__((aligned(256))) uint8_t scratch[kGemmScratchBytes];
 
 namespace {
 
@@ -254,7 +260,43 @@ __global__ __launch_bounds__(256 * H) void k_gemm_xwt(GemmArgs g) {
 
 uint32_t gemm_groups(uint32_t K) { return K % (2u * kGK) == 0 ? 2u : 1u; }
 
+__global__ void k_gemm_clear_counters(uint32_t *cnt) {
+    for (uint32_t i = threadIdx.x; i < kGemmCounters; i += blockDim.x) cnt[i] = 0u;
+}
+
+constexpr int kScratchDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch[kScratchDevices];
+
 }  // namespace
+
+void *gemm_scratch(hipStream_t st, int *err) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess || dev < 0 || dev >= kScratchDevices) {
+        *err = e != hipSuccess ? (int)e : (int)hipErrorInvalidDevice;
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch[dev] == nullptr) {
+        void *p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || p == nullptr) {
+            *err = e != hipSuccess ? (int)e : (int)hipErrorInvalidSymbol;
+            return nullptr;
+        }
+        // the counters start at zero (a kernel, not a memset: the first call may be under graph capture); every
+        // product leaves them zero after that
+        hipLaunchKernelGGL(k_gemm_clear_counters, dim3(1), dim3(256), 0, st, (uint32_t *)p);
+        e = hipGetLastError();
+        if (e != hipSuccess) {
+            *err = (int)e;
+            return nullptr;
+        }
+        g_scratch[dev] = p;
+    }
+    return g_scratch[dev];
+}
 
 uint32_t gemm_splits(uint32_t T, uint32_t N, uint32_t K, int ncu) {
     const uint32_t tiles = ((T + kGT - 1) / kGT) * ((N + kGN - 1) / kGN), units = K / kGK / gemm_groups(K);

@@ -40,7 +40,7 @@ def test_header_declares_the_reference_exports():
     assert d - REFERENCE_EXPORTS == {"nwc_linear_xbf16", "nwc_linear_xbf16_batch", "nwc_row_index", "nwc_token_split",
                                      "nwc_seq_table", "nwc_dequant_seq", "nwc_prefill_xbf16",
                                      "nwc_gather_xindex", "nwc_ref_bf16", "nwc_stream_read", "nwc_gemm_workspace",
-                                     "nwc_gemm_xbf16"}              # this build's additions
+                                     "nwc_gemm_xbf16", "nwc_gemm_xbf16_noalloc"}              # this build's additions
 
 
 def test_binding_signatures_match_the_header():
