@@ -49,9 +49,10 @@ ROW_INDEX = os.environ.get("NWC_ROW_INDEX", "1") != "0"   # layouts 0/1: build t
 # temporary BF16 matrix + F.linear
 BATCH_MAX = int(os.environ.get("NWC_BATCH_MAX", "8"))
 BATCH_LAUNCH = 4                                           # vectors per nwc_linear_xbf16_batch launch
-# more tokens, layout 0: "dequant" (default) decompresses into a temporary BF16 matrix and calls F.linear (hipBLASLt);
-# "fused" runs nwc_prefill_xbf16 (decode into LDS + matrix cores, no temporary matrix; correct, but slower on MI355X
-# at 512 tokens: 20 ms against 8.5 ms per Qwen3-4B stack)
+# more tokens, layout 0: "dequant" (default) decompresses into a temporary BF16 matrix and multiplies it with
+# linear_dequantized (hipBLASLt, or the library's GEMM where that is faster); "fused" runs nwc_prefill_xbf16 (decode
+# into LDS + matrix cores, no temporary matrix; correct, but slower on MI355X at 512 tokens: 19 ms against 8.0 ms
+# per Qwen3-4B stack)
 PREFILL = os.environ.get("NWC_PREFILL", "dequant")
 # the prefill GEMM on the temporary matrix: "auto" (default) the library's split-K matrix-core kernel
 # (nwc_gemm_xbf16) for the shapes where it measured faster than hipBLASLt on MI355X, torch's F.linear for the rest;
