@@ -1056,8 +1056,8 @@ def traffic_bytes():
 
 def run_profile(args):
     """Counter target: --profile-launches launches of one matrix of --config (--profile-shape, default gate_up), after
-    three device copies of 256 MiB (the calibration kernel of known size).  Run under rocprofv3 --pmc; prints one line
-    per phase."""
+    three device copies of 256 MiB (the calibration kernel of known size); with --profile-gemm T, launches of the
+    prefill GEMM on T tokens and that matrix's shape instead.  Run under rocprofv3 --pmc; prints one line per phase."""
     import torch
     from nwc_amd.nwc_torch import NWCWeight
     dev = torch.device("cuda:0")
@@ -1071,6 +1071,17 @@ def run_profile(args):
     _, shapes, elem, layout0, _ = CONFIGS[args.config]
     layout = args.layout if args.config in ("qwen3-4b", "qwen3-4b-fp8") else layout0
     name, M, K = next(s for s in shapes if s[0] == args.profile_shape)
+    if args.profile_gemm:
+        # the prefill GEMM alone (nwc_gemm_xbf16) on --profile-gemm tokens and this matrix's shape
+        from nwc_amd.nwc_torch import gemm_xbf16
+        g = torch.Generator().manual_seed(2)
+        x = torch.randn(args.profile_gemm, K, generator=g).to(torch.bfloat16).to(dev)
+        ws = [(torch.randn(M, K, generator=g) * 0.02).to(torch.bfloat16).to(dev) for _ in range(4)]
+        for i in range(args.profile_launches):
+            gemm_xbf16(x, ws[i % len(ws)])
+        torch.cuda.synchronize()
+        print(f"{name}: {args.profile_launches} launches of nwc_gemm_xbf16, {args.profile_gemm} x {M} x {K}", flush=True)
+        return
     c = NWCWeight(make_weight(M, K, 1000 + [s[0] for s in shapes].index(name)), device=dev, layout=layout, elem=elem)
     cs = [c] + [clone_weight(c) for _ in range(7)]
     x = torch.randn(K, generator=torch.Generator().manual_seed(2)).to(torch.bfloat16).to(dev)
@@ -1100,6 +1111,8 @@ def main():
                     help="only run the counter target (copies + this many gate_up launches), for rocprofv3 --pmc")
     ap.add_argument("--profile-shape", default=DOMINANT, choices=[s[0] for s in SHAPES],
                     help="the Qwen3-4B matrix --profile-launches runs")
+    ap.add_argument("--profile-gemm", type=int, default=0,
+                    help="with --profile-launches: launch the prefill GEMM (nwc_gemm_xbf16) on this many tokens instead")
     ap.add_argument("--config", default="qwen3-4b", choices=sorted(CONFIGS))
     ap.add_argument("--prefill", type=int, default=0, help="time the prefill path for this many tokens instead")
     ap.add_argument("--gather", type=int, default=0, help="time the embedding gather of this many ids instead")
