@@ -267,6 +267,7 @@ __global__ void k_gemm_clear_counters(uint32_t *cnt) {
 constexpr int kScratchDevices = 64;
 std::mutex g_scratch_mu;
 void *g_scratch[kScratchDevices];
+bool g_scratch_clear[kScratchDevices];     // the counters were cleared by a kernel that ran outside graph capture
 
 }  // namespace
 
@@ -285,15 +286,25 @@ void *gemm_scratch(hipStream_t st, int *err) {
             *err = e != hipSuccess ? (int)e : (int)hipErrorInvalidSymbol;
             return nullptr;
         }
-        // the counters start at zero (a kernel, not a memset: the first call may be under graph capture); every
-        // product leaves them zero after that
-        hipLaunchKernelGGL(k_gemm_clear_counters, dim3(1), dim3(256), 0, st, (uint32_t *)p);
+        g_scratch[dev] = p;
+    }
+    if (!g_scratch_clear[dev]) {
+        // The counters start at zero: a kernel clears them (not a memset, which graph capture would record); every
+        // product leaves them zero after that.  Under capture the clear becomes part of the graph, so it is
+        // repeated until a call outside capture has run it.
+        hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+        e = hipStreamIsCapturing(st, &cap);
+        if (e != hipSuccess) {
+            *err = (int)e;
+            return nullptr;
+        }
+        hipLaunchKernelGGL(k_gemm_clear_counters, dim3(1), dim3(256), 0, st, (uint32_t *)g_scratch[dev]);
         e = hipGetLastError();
         if (e != hipSuccess) {
             *err = (int)e;
             return nullptr;
         }
-        g_scratch[dev] = p;
+        if (cap == hipStreamCaptureStatusNone) g_scratch_clear[dev] = true;
     }
     return g_scratch[dev];
 }

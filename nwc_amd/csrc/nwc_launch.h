@@ -40,8 +40,8 @@ constexpr uint64_t kGemmScratchBytes = 24ull << 20;     // nwc_gemm_xbf16_noallo
 uint32_t gemm_splits(uint32_t T, uint32_t N, uint32_t K, int ncu);
 uint64_t gemm_workspace_bytes(uint32_t T, uint32_t N, uint32_t K, int ncu);
 int launch_gemm_xwt(GemmArgs g, void *ws, int ncu, hipStream_t st);
-// the current device's copy of the library's static workspace (its counters cleared on `st` at the first call on
-// the device), or null with *err set
+// the current device's copy of the library's static workspace (its counters cleared on `st` by the first call on
+// the device outside graph capture, and by every captured call before that), or null with *err set
 void *gemm_scratch(hipStream_t st, int *err);
 int launch_ref_fp8(const uint8_t *w, const float *scale, const float *x, uint16_t *y, uint32_t M, uint32_t K, int ncu,
                    hipStream_t st);

@@ -49,3 +49,22 @@ def test_noalloc_unsplit_and_refused(cuda):
     y = torch.zeros(4, 8, dtype=torch.bfloat16, device="cuda")
     with pytest.raises(RuntimeError):                         # K not a multiple of 64
         call("nwc_gemm_xbf16_noalloc", stream(), ptr(x), 128, ptr(w), 128, None, ptr(y), 4, 8, 100)
+
+
+def test_noalloc_graph_replays(cuda):
+    """A captured call replayed three times, eager calls of another shape between the replays: every replay gives
+    the eager result."""
+    print("noalloc graph replays", flush=True)
+    ops = _operands(256, 2560, 9728, seed=7, bias=True)
+    want = _noalloc(*ops)
+    other = _operands(128, 512, 8192, seed=8, bias=False)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        y = _noalloc(*ops)
+    for _ in range(3):
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y.view(torch.int16), want.view(torch.int16))
+        _noalloc(*other)
+        torch.cuda.synchronize()
