@@ -123,7 +123,7 @@ _GEMM_WS_RETIRED = []
 
 def gemm_usable(x: torch.Tensor, weight: torch.Tensor) -> bool:
     """Whether gemm_xbf16 takes this product: BF16 on the GPU, K a multiple of 64, rows of 16-byte multiples."""
-    return (x.dtype == torch.bfloat16 and weight.dtype == torch.bfloat16 and x.is_cuda
+    return (x.dtype == torch.bfloat16 and weight.dtype == torch.bfloat16 and x.is_cuda and x.device == weight.device
             and weight.dim() == 2 and weight.shape[1] % 64 == 0 and weight.stride(1) == 1
             and weight.stride(0) % 8 == 0 and weight.data_ptr() % 16 == 0)
 
@@ -139,8 +139,8 @@ def linear_dequantized(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor
     """The prefill product on a dequantized matrix, F.linear(x, weight, bias): the library GEMM (gemm_xbf16) where
     NWC_GEMM and gemm_preferred choose it, torch's F.linear (hipBLASLt) otherwise.  The choice depends on the shapes
     only, so a dequantized matrix and the same matrix resident in BF16 go through the same GEMM."""
-    if gemm_usable(x, weight) and (GEMM == "nwc" or (GEMM == "auto" and gemm_preferred(
-            x.numel() // weight.shape[1], weight.shape[0], weight.shape[1]))):
+    chosen = GEMM == "nwc" or (GEMM == "auto" and gemm_preferred(x.numel() // weight.shape[1], *weight.shape))
+    if chosen and gemm_usable(x, weight) and (bias is None or bias.device == weight.device):
         return gemm_xbf16(x, weight, bias)
     return F.linear(x, weight, bias)
 
@@ -150,6 +150,9 @@ def gemm_xbf16(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor = None)
     weight [N, K] (a row-strided view such as dequant()'s is fine), bias [N] or None; fp32 accumulation, one RNE
     rounding of the sum + bias.  The partial sums are added in a fixed order: equal inputs give equal bits."""
     _need_gpu(weight)
+    for name, t in (("x", x), ("bias", bias)):
+        if t is not None and t.device != weight.device:
+            raise RuntimeError(f"gemm_xbf16: {name} is on {t.device}, the weight on {weight.device}")
     N, K = weight.shape
     xs = x.reshape(-1, K)
     if xs.stride(-1) != 1 or xs.stride(0) % 8 or xs.data_ptr() % 16:
