@@ -250,7 +250,38 @@ constexpr uint32_t kDynLdsOne = 128u * 1024u;         // dynamic LDS of a workgr
 constexpr uint32_t kDynLdsOne13 = 126u * 1024u;       // the same next to the 13-bit table
 bool plan_layout1_budget(const Shape &f, int mode, int ncu, bool index, uint32_t budget, uint32_t one, Stage stage,
                          LaunchPlan &p);
+// Dequantization of a layout-1 matrix with fewer row groups than two per CU: tiles of whole blocks instead of whole row
+// groups (G = blocks | 1 << 31), two per CU, so every CU works (there are no row sums to combine): 2560 x 9728 has
+// 160 row groups of 19 blocks for 256 CUs, 507 tiles of 6 blocks.  Four (or two) half-waves per block, which needs
+// the row index; the 13-bit table when given.
+bool plan_layout1_blocks(const Shape &f, int ncu, bool seq, LaunchPlan &p) {
+    const uint32_t nb = f.nb, n = 2u * (uint32_t)ncu, BT = std::max(1u, (nb + n - 1u) / n);
+    for (int pass = 0; pass < 2; pass++) {
+        const bool t13 = pass == 0;
+        if (t13 && !seq) continue;
+        const uint32_t budget = t13 ? kDynLds13 : kDynLdsPipe;
+        if (BT * kSlotWords1Min * 4u > budget) continue;
+        for (uint32_t sp : {4u, 2u}) {
+            const uint32_t halves = (BT * sp + 1u) & ~1u;
+            if (halves > 32u) continue;
+            const uint32_t slot = std::min(kSlotWords1s, budget / (4u * BT));
+            p = LaunchPlan{};
+            p.layout = 1;
+            p.seq13 = t13;
+            p.split = sp;
+            p.G = BT | 0x80000000u;
+            p.threads = 32u * halves;
+            p.grid = (nb + BT - 1u) / BT;
+            p.slot_words = slot;
+            p.lds = BT * slot * 4u;
+            return true;
+        }
+    }
+    return false;
+}
+
 bool plan_layout1(const Shape &f, int mode, int ncu, bool index, bool seq, LaunchPlan &p) {
+    if (mode == kDequant && index && f.groups() < 2u * (uint32_t)ncu && plan_layout1_blocks(f, ncu, seq, p)) return true;
     const bool t13 = seq && ((mode == kToken && index) || mode == kDequant);
     for (Stage stage : {kOneRound, kRounds}) {
         if (t13 && plan_layout1_budget(f, mode, ncu, index, kDynLds13, kDynLdsOne13, stage, p)) {

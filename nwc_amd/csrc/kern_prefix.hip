@@ -923,21 +923,26 @@ __device__ __forceinline__ void layout1s_body(BlockArgs a, uint32_t nth, uint32_
     const uint32_t tid = threadIdx.x, L = tid & 31;
     const uint32_t hw = tid >> 5;
     const Shape f(a.M, a.K, 1);
-    const uint32_t cap = a.slot_words * a.G * f.CB;            // the plan's region: one slot per block of the tile
+    // Dequantization may take a range of blocks instead of whole row groups (bit 31 of G set, G & 0x7FFFFFFF blocks
+    // per workgroup): with no row sums to combine, a tile may start and end inside a row group.
+    const bool bt = MODE == kDequant && (a.G >> 31) != 0u;
+    const uint32_t gsz = a.G & 0x7FFFFFFFu;
+    const uint32_t cap = a.slot_words * (bt ? gsz : gsz * f.CB);   // the plan's region: one slot per block of the tile
     const uint32_t n8 = (f.K16 + 31u) / 32u * 4u;               // x: K32 BF16 values, in chunks of eight
     uint32_t *cur = dyn;
     uint4 *xs = (uint4 *)(dyn + cap);
     float *part = (float *)(xs + (ROWS ? n8 : 0u));
-    const uint32_t rg0 = blockIdx.x * a.G;
-    const uint32_t ng = min(a.G, f.groups() - rg0);
-    const uint32_t nt = ng * f.CB, tl = nt - 1u;
-    const uint32_t B0 = rg0 * f.CB, nb = f.nb;
+    const uint32_t nb = f.nb;
+    const uint32_t rg0 = bt ? 0u : blockIdx.x * gsz;
+    const uint32_t ng = bt ? 0u : min(gsz, f.groups() - rg0);
+    const uint32_t B0 = bt ? blockIdx.x * gsz : rg0 * f.CB;
+    const uint32_t nt = bt ? min(gsz, nb - B0) : ng * f.CB, tl = nt - 1u;
     const uint32_t mend = !a.stride && B0 + nt == nb ? matrix_end(a, nb) : 0u;
     Region R = region_of(a, B0, B0 + nt, nb, mend, a.stride);
     TabStage<PEEK> Q;
     Q.issue(a, nth);
     const uint32_t t = hw / SP, p = hw % SP, sc0 = p * NS;
-    const Coord1 c = coord1<ELEM>(min(t, tl), rg0, f, L);
+    const Coord1 c = coord1<ELEM>((bt ? B0 : 0u) + min(t, tl), rg0, f, L);   // with bt: rg0 = 0, absolute block
     const uint32_t n = a.hdr[(uint64_t)c.b * kHdrBytes + L], base = block_base(a, c.b);
     Bulk Bk;
     bulk_issue(Bk, a.data, R, tid, nth);
