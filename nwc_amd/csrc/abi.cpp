@@ -250,12 +250,15 @@ constexpr uint32_t kDynLdsOne = 128u * 1024u;         // dynamic LDS of a workgr
 constexpr uint32_t kDynLdsOne13 = 126u * 1024u;       // the same next to the 13-bit table
 bool plan_layout1_budget(const Shape &f, int mode, int ncu, bool index, uint32_t budget, uint32_t one, Stage stage,
                          LaunchPlan &p);
-// Dequantization of a layout-1 matrix with fewer row groups than two per CU: tiles of whole blocks instead of whole row
-// groups (G = blocks | 1 << 31), two per CU, so every CU works (there are no row sums to combine): 2560 x 9728 has
-// 160 row groups of 19 blocks for 256 CUs, 507 tiles of 6 blocks.  Four (or two) half-waves per block, which needs
-// the row index; the 13-bit table when given.
+// Dequantization of a layout-1 matrix in one round: tiles of whole blocks instead of whole row groups (G = blocks |
+// 1 << 31), two per CU, so every CU decodes about the same number of blocks (there are no row sums to combine):
+// 2560 x 9728 has 160 row groups of 19 blocks for 256 CUs, 507 tiles of 6 blocks; 19456 x 2560 1216 row groups of 5,
+// 507 tiles of 12 (whole row groups: 406 tiles of 3, so some CUs decode 6 row groups and others 3).  Four (or two)
+// half-waves per block, which needs the row index, at most 32 per workgroup; the 13-bit table when given.  Larger
+// matrices keep the row-group plans.
 bool plan_layout1_blocks(const Shape &f, int ncu, bool seq, LaunchPlan &p) {
     const uint32_t nb = f.nb, n = 2u * (uint32_t)ncu, BT = std::max(1u, (nb + n - 1u) / n);
+    if (BT > 16u) return false;
     for (int pass = 0; pass < 2; pass++) {
         const bool t13 = pass == 0;
         if (t13 && !seq) continue;
@@ -281,7 +284,7 @@ bool plan_layout1_blocks(const Shape &f, int ncu, bool seq, LaunchPlan &p) {
 }
 
 bool plan_layout1(const Shape &f, int mode, int ncu, bool index, bool seq, LaunchPlan &p) {
-    if (mode == kDequant && index && f.groups() < 2u * (uint32_t)ncu && plan_layout1_blocks(f, ncu, seq, p)) return true;
+    if (mode == kDequant && index && plan_layout1_blocks(f, ncu, seq, p)) return true;
     const bool t13 = seq && ((mode == kToken && index) || mode == kDequant);
     for (Stage stage : {kOneRound, kRounds}) {
         if (t13 && plan_layout1_budget(f, mode, ncu, index, kDynLds13, kDynLdsOne13, stage, p)) {
