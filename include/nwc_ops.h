@@ -175,9 +175,9 @@ int nwc_gemm_xbf16(void *stream, const uint16_t *x, uint32_t ldx, const uint16_t
  * capture, tight serving loops, harnesses that forbid hipMalloc); no counterpart in the reference.  The partial sums
  * live in a static array of the library, 24 MiB on each GPU it runs on, held until the process ends (its counters
  * are cleared by a small kernel on `stream` at the first call on a device outside graph capture, and by every
- * captured call before that one).  A product whose workspace would exceed
- * 24 MiB returns -1.  Every call on one GPU shares that array, so calls that overlap on one GPU (two streams) race.
- * Allocates nothing; same results as nwc_gemm_xbf16. */
+ * captured call before that one).  A product whose workspace would exceed 24 MiB returns -1.  Every call on one GPU
+ * shares that array, so calls that overlap on one GPU (two streams) race.  Allocates nothing; same results as
+ * nwc_gemm_xbf16. */
 int nwc_gemm_xbf16_noalloc(void *stream, const uint16_t *x, uint32_t ldx, const uint16_t *w, uint32_t ldw,
                            const uint16_t *bias, uint16_t *y, uint32_t T, uint32_t N, uint32_t K);
 
